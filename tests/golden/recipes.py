@@ -1,0 +1,66 @@
+"""Seeded synthetic inputs shared by the fixture writer, the tests and bench.py.
+
+Everything is drawn from the torch CPU generator, so the same seed gives the
+same tensor on any machine running this image. Only the recipe and the seeds
+are committed; the arrays are regenerated where they are needed.
+"""
+from __future__ import annotations
+
+import torch
+
+
+def gaussian_weight(rows: int, cols: int, seed: int, sigma: float = 0.02,
+                    outlier_frac: float = 0.001, outlier_gain: float = 20.0,
+                    dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """N(0, sigma) weights with `outlier_frac` of positions scaled by `outlier_gain`."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(rows, cols, generator=g) * sigma
+    n_hot = int(rows * cols * outlier_frac)
+    if n_hot > 0:
+        idx = torch.randperm(rows * cols, generator=g)[:n_hot]
+        w.view(-1)[idx] *= outlier_gain
+    return w.to(dtype)
+
+
+def student_t_weight(rows: int, cols: int, seed: int, df: int = 5, sigma: float = 0.02,
+                     dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """Student-t(df) x sigma weights: z / sqrt(chi2_df / df)."""
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn(rows, cols, generator=g)
+    c = torch.zeros(rows, cols)
+    for _ in range(df):
+        c += torch.randn(rows, cols, generator=g) ** 2
+    return (z / torch.sqrt(c / df) * sigma).to(dtype)
+
+
+def tie_heavy_weight(rows: int, cols: int, seed: int, levels: int = 64,
+                     dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """Weights drawn from a small discrete set, so the top-k threshold is
+    shared by many positions (exercises the top-k tie order)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randint(-levels, levels + 1, (rows, cols), generator=g).to(torch.float32)
+    return (q / levels * 0.05).to(dtype)
+
+
+def activations(m: int, k: int, seed: int = 7, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Activations x ~ N(0, 1) in bf16."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(m, k, generator=g).to(dtype)
+
+
+# Llama-3-8B-shaped decoder-layer linears: (name, out_features, in_features).
+LLAMA3_8B_LINEARS = (
+    ("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+    ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336),
+)
+
+# Llama-3-70B-shaped layer linears.
+LLAMA3_70B_LINEARS = (
+    ("q", 8192, 8192), ("k", 1024, 8192), ("v", 1024, 8192), ("o", 8192, 8192),
+    ("gate", 28672, 8192), ("up", 28672, 8192), ("down", 8192, 28672),
+)
+
+
+def layer_seed(index: int) -> int:
+    """Seed for linear number `index` (q, k, v, o, gate, up, down = 0..6)."""
+    return 1000 + index
