@@ -1,0 +1,198 @@
+// extern "C" entry points of libtensorshrink_hip.so (declared in
+// include/tensorshrink_hip.h). Argument checking and dispatch only; the
+// kernels live in ts_decode.hip, ts_prefill.hip, ts_aux.hip, ts_quantize.hip.
+#include "ts_common.h"
+
+namespace ts {
+int decode_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
+                   int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st);
+int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
+                    int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st);
+int generic_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
+                    int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st);
+int dequantize(const ts_qlayer* L, int mode, const int32_t* oidx, const uint16_t* oval, int64_t n_oidx,
+               void* w_out, int64_t ldw, int dt, hipStream_t st);
+int outlier_row_ptr(const int32_t* row, int64_t n, int64_t rows, int32_t* row_ptr, hipStream_t st);
+size_t outlier_tables_ws(int64_t n);
+int build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n, int32_t* orow,
+                         int32_t* ocol, uint16_t* odelta, int32_t* row_ptr, void* ws, size_t ws_bytes,
+                         hipStream_t st);
+int apply_outlier_correction(float* out, int64_t M, int64_t ldo, const void* x, int64_t ldx, int xdt,
+                             const int32_t* row_ptr, const int32_t* col, const uint16_t* delta, int64_t rows,
+                             hipStream_t st);
+size_t topk_ws_bytes(int64_t n, int64_t k);
+int topk_count(const ts_qinput* in, int64_t k, void* ws, size_t ws_bytes, int64_t* n_cand, hipStream_t st);
+int topk_write(const ts_qinput* in, int64_t k, void* ws, int64_t* cidx, float* cval, hipStream_t st);
+int topk_select(const int64_t* cidx, const float* cval, int64_t nc, int64_t n, int64_t k, int64_t* out_idx,
+                float* out_val);
+int quantize_groups(const ts_qinput* in, const ts_group_opts* o, uint8_t* packed, int64_t pstride, uint16_t* s16,
+                    uint16_t* g16, float* s32, float* g32, hipStream_t st);
+int lm_sample(const ts_qinput* in, const ts_group_opts* o, const float* s32, const float* g32, const int64_t* idx,
+              int64_t n, float* out, hipStream_t st);
+int lloyd_max_fit_host(const float* x, int64_t m, const float* init, int32_t n_levels, int32_t iters, float* out);
+int double_quantize(const uint16_t* v, int64_t n, int64_t dqgs, uint8_t* codes, uint16_t* meta, uint16_t* recon,
+                    hipStream_t st);
+int rvq_residual(const ts_qinput* in, const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n,
+                 float* res, hipStream_t st);
+int sq_error_sums(const ts_qinput* in, const void* d, int ddt, double* sums, hipStream_t st);
+int gather_f16(const void* w, int dt, const int64_t* idx, int64_t n, uint16_t* out, hipStream_t st);
+}  // namespace ts
+
+static inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+static bool layer_ok(const ts_qlayer* L) {
+  if (!L || !L->packed || L->rows <= 0 || L->cols <= 0 || L->group_size <= 0) return false;
+  if (L->bits != 2 && L->bits != 4 && L->bits != 8 && L->bits != 6) return false;
+  if (L->padded_cols < L->cols || L->padded_cols % L->group_size != 0) return false;
+  if (L->n_groups != L->padded_cols / L->group_size) return false;
+  const bool dq = L->dq_scale_codes != nullptr;
+  if (dq && (!L->dq_scale_meta || !L->dq_gmin_codes || !L->dq_gmin_meta || L->dq_group_size <= 0)) return false;
+  if (!dq && (!L->scale || !L->gmin)) return false;
+  if (L->n_outliers > 0 && (!L->outlier_row || !L->outlier_col || !L->outlier_delta || !L->outlier_row_ptr))
+    return false;
+  if (L->bits == 6 && (!L->stage2_packed || !L->stage2_scale || !L->stage2_gmin)) return false;
+  return true;
+}
+
+extern "C" {
+
+const char* ts_status_str(int s) {
+  switch (s) {
+    case TS_OK: return "ok";
+    case TS_NOT_COVERED: return "shape or format not covered by the kernels";
+    case TS_BAD_ARG: return "bad argument";
+    case TS_HIP_ERROR: return "HIP runtime error";
+    case TS_WORKSPACE: return "workspace too small";
+    default: return "unknown status";
+  }
+}
+
+const char* ts_version(void) { return "tensorshrink_hip 0.1.0 (gfx950)"; }
+
+size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M) {
+  (void)layer;
+  (void)M;
+  return 0;
+}
+
+int ts_qlinear_forward(const ts_qlayer* L, const void* x, int64_t M, int64_t ldx, int x_dtype, void* y, int64_t ldy,
+                       int y_dtype, const void* bias, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  if (!layer_ok(L) || !x || !y || M < 0) return TS_BAD_ARG;
+  if (x_dtype != TS_BF16 && x_dtype != TS_F16) return TS_BAD_ARG;
+  if (y_dtype != TS_BF16 && y_dtype != TS_F16 && y_dtype != TS_F32) return TS_BAD_ARG;
+  if (y_dtype != TS_F32 && y_dtype != x_dtype) return TS_BAD_ARG;
+  if (ldx < L->cols || ldy < L->rows) return TS_BAD_ARG;
+  if (M == 0) return TS_OK;
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* bp = static_cast<const uint16_t*>(bias);
+  // The tiled kernels read x in aligned 16-byte chunks.
+  const bool aligned = (L->cols % 8 == 0) && (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  int rc = TS_NOT_COVERED;
+  if (aligned) {
+    if (M <= 16) rc = ts::decode_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
+    else rc = ts::prefill_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
+  }
+  if (rc == TS_NOT_COVERED) rc = ts::generic_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
+  return rc;
+}
+
+int ts_apply_outlier_correction(float* out, int64_t M, int64_t ldo, const void* x, int64_t ldx, int x_dtype,
+                                const int32_t* row_ptr, const int32_t* col, const uint16_t* delta, int64_t rows,
+                                void* stream) {
+  if (!out || !x || !row_ptr || !col || !delta || M < 0 || rows < 0) return TS_BAD_ARG;
+  if (x_dtype != TS_BF16 && x_dtype != TS_F16) return TS_BAD_ARG;
+  return ts::apply_outlier_correction(out, M, ldo, x, ldx, x_dtype, row_ptr, col, delta, rows, S(stream));
+}
+
+int ts_dequantize(const ts_qlayer* L, int mode, const int32_t* outlier_idx, const uint16_t* outlier_val,
+                  int64_t n_outlier_idx, void* w_out, int64_t ldw, int out_dtype, void* stream) {
+  if (!layer_ok(L) || !w_out || ldw < L->cols) return TS_BAD_ARG;
+  if (mode != TS_DEQ_CODEC && mode != TS_DEQ_QLINEAR) return TS_BAD_ARG;
+  if (mode == TS_DEQ_CODEC && n_outlier_idx > 0 && (!outlier_idx || !outlier_val)) return TS_BAD_ARG;
+  if (out_dtype != TS_F16 && out_dtype != TS_BF16 && out_dtype != TS_F32) return TS_BAD_ARG;
+  return ts::dequantize(L, mode, outlier_idx, outlier_val, n_outlier_idx, w_out, ldw, out_dtype, S(stream));
+}
+
+int ts_outlier_row_ptr(const int32_t* outlier_row, int64_t n, int64_t rows, int32_t* row_ptr, void* stream) {
+  if ((n > 0 && !outlier_row) || !row_ptr || rows < 0) return TS_BAD_ARG;
+  return ts::outlier_row_ptr(outlier_row, n, rows, row_ptr, S(stream));
+}
+
+size_t ts_outlier_tables_workspace_bytes(int64_t n, int64_t rows) {
+  (void)rows;
+  return n > 0 ? ts::outlier_tables_ws(n) : 0;
+}
+
+int ts_build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n, int32_t* orow,
+                            int32_t* ocol, uint16_t* odelta, int32_t* row_ptr, void* ws, size_t ws_bytes,
+                            void* stream) {
+  if (!L || !L->packed || n < 0 || (n > 0 && (!idx || !val || !orow || !ocol || !odelta))) return TS_BAD_ARG;
+  if (n > 0 && (L->rows * L->cols) > ((int64_t)1 << 31)) return TS_NOT_COVERED;  // int32 flat indices
+  return ts::build_outlier_tables(L, idx, val, n, orow, ocol, odelta, row_ptr, ws, ws_bytes, S(stream));
+}
+
+size_t ts_topk_workspace_bytes(int64_t n, int64_t k) { return (k > 0 && k < n) ? ts::topk_ws_bytes(n, k) : 0; }
+
+int ts_topk_candidates_count(const ts_qinput* in, int64_t k, void* ws, size_t ws_bytes, int64_t* n_candidates,
+                             void* stream) {
+  if (!in || !in->w || in->rows <= 0 || in->cols <= 0 || !n_candidates) return TS_BAD_ARG;
+  return ts::topk_count(in, k, ws, ws_bytes, n_candidates, S(stream));
+}
+
+int ts_topk_candidates_write(const ts_qinput* in, int64_t k, void* ws, int64_t* cand_idx, float* cand_val,
+                             void* stream) {
+  if (!in || !in->w || !ws || !cand_idx || !cand_val) return TS_BAD_ARG;
+  return ts::topk_write(in, k, ws, cand_idx, cand_val, S(stream));
+}
+
+int ts_topk_select(const int64_t* cand_idx, const float* cand_val, int64_t n_candidates, int64_t n, int64_t k,
+                   int64_t* out_idx, float* out_val) {
+  if (!cand_idx || !cand_val || !out_idx || !out_val) return TS_BAD_ARG;
+  return ts::topk_select(cand_idx, cand_val, n_candidates, n, k, out_idx, out_val);
+}
+
+int ts_quantize_groups(const ts_qinput* in, const ts_group_opts* opts, uint8_t* packed, int64_t packed_stride,
+                       uint16_t* scale16, uint16_t* gmin16, float* scale32, float* gmin32, void* stream) {
+  if (!in || !in->w || !opts || !packed || !scale16 || !gmin16) return TS_BAD_ARG;
+  if (opts->bits != 2 && opts->bits != 4 && opts->bits != 8) return TS_BAD_ARG;
+  if (opts->group_size <= 0 || (scale32 == nullptr) != (gmin32 == nullptr)) return TS_BAD_ARG;
+  return ts::quantize_groups(in, opts, packed, packed_stride, scale16, gmin16, scale32, gmin32, S(stream));
+}
+
+int ts_lm_sample(const ts_qinput* in, const ts_group_opts* opts, const float* scale32, const float* gmin32,
+                 const int64_t* idx, int64_t n, float* out, void* stream) {
+  if (!in || !opts || !scale32 || !gmin32 || (n > 0 && (!idx || !out))) return TS_BAD_ARG;
+  return ts::lm_sample(in, opts, scale32, gmin32, idx, n, out, S(stream));
+}
+
+int ts_lloyd_max_fit_host(const float* samples, int64_t m, const float* linspace_init, int32_t n_levels,
+                          int32_t iters, float* out_centroids) {
+  if (!samples || !linspace_init || !out_centroids) return TS_BAD_ARG;
+  return ts::lloyd_max_fit_host(samples, m, linspace_init, n_levels, iters, out_centroids);
+}
+
+int ts_double_quantize(const uint16_t* values16, int64_t n, int64_t dq_group_size, uint8_t* codes, uint16_t* meta,
+                       uint16_t* recon16, void* stream) {
+  if (!values16 || !codes || !meta) return TS_BAD_ARG;
+  return ts::double_quantize(values16, n, dq_group_size, codes, meta, recon16, S(stream));
+}
+
+int ts_rvq_residual(const ts_qinput* in, const ts_qlayer* stage1, const int32_t* outlier_idx,
+                    const uint16_t* outlier_val, int64_t n_outliers, float* residual, void* stream) {
+  if (!in || !stage1 || !residual || stage1->bits != 4) return TS_BAD_ARG;
+  return ts::rvq_residual(in, stage1, outlier_idx, outlier_val, n_outliers, residual, S(stream));
+}
+
+int ts_sq_error_sums(const ts_qinput* in, const void* deq, int deq_dtype, double* sums2, void* stream) {
+  if (!in || !deq || !sums2) return TS_BAD_ARG;
+  return ts::sq_error_sums(in, deq, deq_dtype, sums2, S(stream));
+}
+
+int ts_gather_f16(const void* w, int w_dtype, const int64_t* idx, int64_t n, uint16_t* out, void* stream) {
+  if (n > 0 && (!w || !idx || !out)) return TS_BAD_ARG;
+  return ts::gather_f16(w, w_dtype, idx, n, out, S(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,236 @@
+// Dense dequantization, QuantLinear outlier tables and the standalone outlier
+// correction. Everything here that the reference defines bit-for-bit
+// (dequantize_tensor, _outlier_base_val, _compute_outlier_delta) keeps the
+// reference's float32 operation order: separate multiply and add, no FMA
+// contraction, round-to-nearest-even narrowing.
+#include <cstring>
+
+#include <rocprim/rocprim.hpp>
+
+#include "ts_common.h"
+
+namespace ts {
+
+// Code value at (row, col) of a packed layer: the raw code or codebook[code]
+// as float32 (modules.py:664-694, codec.py:775-788).
+TS_DEV float code_value(const ts_qlayer& L, int64_t row, int64_t col) {
+  const uint8_t* p = L.packed + row * L.packed_stride;
+  uint32_t c;
+  if (L.bits == 2) c = (p[col >> 2] >> (2 * (col & 3))) & 3u;
+  else if (L.bits == 4 || L.bits == 6) c = (p[col >> 1] >> (4 * (col & 1))) & 15u;
+  else c = p[col];
+  if (L.codebook && L.bits != 6) return L.codebook[c];
+  return (float)c;
+}
+
+// float32 scale/gmin of (row, group): DQ reconstruction codes*ms + mm
+// (codec.py:420-435 / modules.py:573-579) or the f16 values.
+TS_DEV void scale_gmin_f32(const ts_qlayer& L, int64_t row, int64_t g, float& s, float& gm) {
+#pragma clang fp contract(off)
+  const int64_t flat = row * L.n_groups + g;
+  if (L.dq_scale_codes) {
+    const int64_t sup = flat / L.dq_group_size;
+    s = (float)L.dq_scale_codes[flat] * ts_h2f(L.dq_scale_meta[2 * sup]) + ts_h2f(L.dq_scale_meta[2 * sup + 1]);
+    gm = (float)L.dq_gmin_codes[flat] * ts_h2f(L.dq_gmin_meta[2 * sup]) + ts_h2f(L.dq_gmin_meta[2 * sup + 1]);
+  } else {
+    s = ts_h2f(L.scale[flat]);
+    gm = ts_h2f(L.gmin[flat]);
+  }
+}
+
+TS_DEV float base_value(const ts_qlayer& L, int64_t row, int64_t col) {
+#pragma clang fp contract(off)
+  const int64_t g = col / L.group_size;
+  float s, gm;
+  scale_gmin_f32(L, row, g, s, gm);
+  const float cv = code_value(L, row, col);
+  return cv * s + gm;
+}
+
+// RVQ stage 2 value (codec.py:836-844): uniform 2-bit, f16 scale/gmin.
+TS_DEV float stage2_value(const ts_qlayer& L, int64_t row, int64_t col) {
+#pragma clang fp contract(off)
+  const uint8_t* p = L.stage2_packed + row * L.stage2_stride;
+  const float c = (float)((p[col >> 2] >> (2 * (col & 3))) & 3u);
+  const int64_t flat = row * L.n_groups + col / L.group_size;
+  return c * ts_h2f(L.stage2_scale[flat]) + ts_h2f(L.stage2_gmin[flat]);
+}
+
+TS_DEV void store_out(void* out, int64_t off, int dt, float v) {
+  if (dt == TS_F32) reinterpret_cast<float*>(out)[off] = v;
+  else if (dt == TS_BF16) reinterpret_cast<uint16_t*>(out)[off] = ts_f2bf(v);
+  else reinterpret_cast<uint16_t*>(out)[off] = ts_f2h(v);
+}
+
+// Pass 1: every position gets cast(base (+ RVQ stage 2)).
+__global__ void dequant_base_kernel(const ts_qlayer L, void* out, int64_t ldw, int dt) {
+#pragma clang fp contract(off)
+  const int64_t row = blockIdx.y;
+  for (int64_t col = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; col < L.cols;
+       col += (int64_t)gridDim.x * blockDim.x) {
+    float v = base_value(L, row, col);
+    if (L.bits == 6) v = v + stage2_value(L, row, col);
+    store_out(out, row * ldw + col, dt, v);
+  }
+}
+
+// Pass 2, codec view (codec.py:793-796, 823-846): the outlier position takes
+// f32(outlier_val) (+ RVQ stage 2), then the cast.
+__global__ void dequant_outlier_codec_kernel(const ts_qlayer L, void* out, int64_t ldw, int dt, const int32_t* idx,
+                                             const uint16_t* val, int64_t n) {
+#pragma clang fp contract(off)
+  const int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (o >= n) return;
+  const int64_t f = idx[o];
+  const int64_t r = f / L.cols, c = f % L.cols;
+  float v = ts_h2f(val[o]);
+  if (L.bits == 6) v = v + stage2_value(L, r, c);
+  store_out(out, r * ldw + c, dt, v);
+}
+
+// Pass 2, QuantLinear view (modules.py:786-802 in float32): base + delta.
+__global__ void dequant_outlier_qlinear_kernel(const ts_qlayer L, void* out, int64_t ldw, int dt) {
+#pragma clang fp contract(off)
+  const int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (o >= L.n_outliers) return;
+  const int64_t r = L.outlier_row[o], c = L.outlier_col[o];
+  float v = base_value(L, r, c) + ts_h2f(L.outlier_delta[o]);
+  if (L.bits == 6) v = v + stage2_value(L, r, c);
+  store_out(out, r * ldw + c, dt, v);
+}
+
+// row_ptr[r] = first k with row[k] >= r (lower bound), r in [0, rows].
+__global__ void row_ptr_kernel(const int32_t* row, int64_t n, int64_t rows, int32_t* row_ptr) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r > rows) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (row[mid] < r) lo = mid + 1;
+    else hi = mid;
+  }
+  row_ptr[r] = (int32_t)lo;
+}
+
+__global__ void split_idx_kernel(const int32_t* idx, int64_t n, int64_t cols, uint32_t* key, uint32_t* pos) {
+  const int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (o >= n) return;
+  key[o] = (uint32_t)((int64_t)idx[o] / cols);
+  pos[o] = (uint32_t)o;
+}
+
+// Sorted position o <- codec position perm[o]; delta per modules.py:700-715.
+__global__ void outlier_delta_kernel(const ts_qlayer L, const int32_t* idx, const uint16_t* val,
+                                     const uint32_t* perm, int64_t n, int32_t* orow, int32_t* ocol,
+                                     uint16_t* odelta) {
+#pragma clang fp contract(off)
+  const int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (o >= n) return;
+  const int64_t src = perm[o];
+  const int64_t f = idx[src];
+  const int64_t r = f / L.cols;
+  const int64_t c = f % L.cols;
+  orow[o] = (int32_t)r;
+  ocol[o] = (int32_t)c;
+  const float base = base_value(L, r, c);
+  odelta[o] = ts_f2h(ts_h2f(val[src]) - base);
+}
+
+// out[m, r] += sum over the row's outliers of x[m, col] * delta (row-sorted
+// CSR; one thread per (m, row), no atomics).
+template <bool BF16>
+__global__ void outlier_correction_kernel(float* out, int64_t M, int64_t ldo, const uint16_t* x, int64_t ldx,
+                                          const int32_t* row_ptr, const int32_t* col, const uint16_t* delta,
+                                          int64_t rows) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t m = blockIdx.y;
+  if (r >= rows || m >= M) return;
+  const int32_t o0 = row_ptr[r], o1 = row_ptr[r + 1];
+  if (o0 == o1) return;
+  float acc = 0.f;
+  for (int32_t o = o0; o < o1; ++o) acc += XT<BF16>::to_f(x[m * ldx + col[o]]) * ts_h2f(delta[o]);
+  out[m * ldo + r] += acc;
+}
+
+int dequantize(const ts_qlayer* Lp, int mode, const int32_t* oidx, const uint16_t* oval, int64_t n_oidx,
+               void* w_out, int64_t ldw, int dt, hipStream_t st) {
+  const ts_qlayer& L = *Lp;
+  dim3 grid((unsigned)std::min<int64_t>(ts_cdiv(L.cols, 256), 64), (unsigned)L.rows);
+  hipLaunchKernelGGL(dequant_base_kernel, grid, dim3(256), 0, st, L, w_out, ldw, dt);
+  TS_CHECK_LAUNCH();
+  if (mode == TS_DEQ_CODEC && n_oidx > 0) {
+    hipLaunchKernelGGL(dequant_outlier_codec_kernel, dim3((unsigned)ts_cdiv(n_oidx, 256)), dim3(256), 0, st, L,
+                       w_out, ldw, dt, oidx, oval, n_oidx);
+    TS_CHECK_LAUNCH();
+  } else if (mode == TS_DEQ_QLINEAR && L.n_outliers > 0) {
+    hipLaunchKernelGGL(dequant_outlier_qlinear_kernel, dim3((unsigned)ts_cdiv(L.n_outliers, 256)), dim3(256), 0,
+                       st, L, w_out, ldw, dt);
+    TS_CHECK_LAUNCH();
+  }
+  return TS_OK;
+}
+
+int outlier_row_ptr(const int32_t* row, int64_t n, int64_t rows, int32_t* row_ptr, hipStream_t st) {
+  hipLaunchKernelGGL(row_ptr_kernel, dim3((unsigned)ts_cdiv(rows + 1, 256)), dim3(256), 0, st, row, n, rows,
+                     row_ptr);
+  TS_CHECK_LAUNCH();
+  return TS_OK;
+}
+
+size_t outlier_tables_ws(int64_t n) {
+  size_t sort_bytes = 0;
+  (void)rocprim::radix_sort_pairs(nullptr, sort_bytes, (uint32_t*)nullptr, (uint32_t*)nullptr,
+                                                (uint32_t*)nullptr, (uint32_t*)nullptr, (size_t)n, 0, 32);
+  const size_t arr = ((size_t)n * 4 + 255) / 256 * 256;
+  return 4 * arr + (sort_bytes + 255) / 256 * 256 + 256;
+}
+
+int build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n, int32_t* orow,
+                         int32_t* ocol, uint16_t* odelta, int32_t* row_ptr, void* ws, size_t ws_bytes,
+                         hipStream_t st) {
+  if (n == 0) {
+    if (row_ptr) return outlier_row_ptr(orow, 0, L->rows, row_ptr, st);
+    return TS_OK;
+  }
+  if (ws_bytes < outlier_tables_ws(n)) return TS_WORKSPACE;
+  const size_t arr = ((size_t)n * 4 + 255) / 256 * 256;
+  char* p = static_cast<char*>(ws);
+  uint32_t* key_in = reinterpret_cast<uint32_t*>(p);
+  uint32_t* key_out = reinterpret_cast<uint32_t*>(p + arr);
+  uint32_t* pos_in = reinterpret_cast<uint32_t*>(p + 2 * arr);
+  uint32_t* pos_out = reinterpret_cast<uint32_t*>(p + 3 * arr);
+  void* tmp = p + 4 * arr;
+  size_t tmp_bytes = ws_bytes - 4 * arr;
+  hipLaunchKernelGGL(split_idx_kernel, dim3((unsigned)ts_cdiv(n, 256)), dim3(256), 0, st, idx, n, L->cols, key_in,
+                     pos_in);
+  TS_CHECK_LAUNCH();
+  int end_bit = 1;
+  while (end_bit < 32 && ((int64_t)1 << end_bit) <= L->rows) ++end_bit;
+  // LSD radix sort is stable: equal rows keep codec (top-k) order, as
+  // np.argsort(kind="stable") does in modules.py:422.
+  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, key_in, key_out, pos_in, pos_out, (size_t)n, 0, end_bit, st) !=
+      hipSuccess)
+    return TS_HIP_ERROR;
+  hipLaunchKernelGGL(outlier_delta_kernel, dim3((unsigned)ts_cdiv(n, 256)), dim3(256), 0, st, *L, idx, val,
+                     pos_out, n, orow, ocol, odelta);
+  TS_CHECK_LAUNCH();
+  if (row_ptr) return outlier_row_ptr(orow, n, L->rows, row_ptr, st);
+  return TS_OK;
+}
+
+int apply_outlier_correction(float* out, int64_t M, int64_t ldo, const void* x, int64_t ldx, int xdt,
+                             const int32_t* row_ptr, const int32_t* col, const uint16_t* delta, int64_t rows,
+                             hipStream_t st) {
+  if (M <= 0 || rows <= 0) return TS_OK;
+  dim3 grid((unsigned)ts_cdiv(rows, 256), (unsigned)M);
+  if (xdt == TS_BF16)
+    hipLaunchKernelGGL(outlier_correction_kernel<true>, grid, dim3(256), 0, st, out, M, ldo,
+                       static_cast<const uint16_t*>(x), ldx, row_ptr, col, delta, rows);
+  else
+    hipLaunchKernelGGL(outlier_correction_kernel<false>, grid, dim3(256), 0, st, out, M, ldo,
+                       static_cast<const uint16_t*>(x), ldx, row_ptr, col, delta, rows);
+  TS_CHECK_LAUNCH();
+  return TS_OK;
+}
+
+}  // namespace ts

@@ -1,0 +1,79 @@
+// Shared device helpers for the gfx950 GOAP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tensorshrink_hip.h"
+
+#define TS_DEV __device__ __forceinline__
+
+typedef __bf16 ts_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 ts_f16x8 __attribute__((ext_vector_type(8)));
+typedef float ts_f32x4 __attribute__((ext_vector_type(4)));
+typedef float ts_f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t ts_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t ts_u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// scalar conversions (IEEE, round to nearest even, subnormals kept)
+// ---------------------------------------------------------------------------
+TS_DEV float ts_h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+TS_DEV uint16_t ts_f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+TS_DEV float ts_bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+TS_DEV uint16_t ts_f2bf(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Activation element type: bf16 or f16 storage as uint16_t.
+template <bool BF16> struct XT;
+template <> struct XT<true> {
+  static TS_DEV float to_f(uint16_t v) { return ts_bf2f(v); }
+  static TS_DEV uint16_t from_f(float f) { return ts_f2bf(f); }
+  static constexpr uint32_t ONE = 0x3f80u;
+};
+template <> struct XT<false> {
+  static TS_DEV float to_f(uint16_t v) { return ts_h2f(v); }
+  static TS_DEV uint16_t from_f(float f) { return ts_f2h(f); }
+  static constexpr uint32_t ONE = 0x3c00u;
+};
+
+// D[16x16] += A[16x32] * B[32x16]. Lane l holds A row l%16, B column l%16,
+// k = 8*(l/16) + i for element i, and D[4*(l/16) + i][l%16] (checked on gfx950).
+template <bool BF16>
+TS_DEV ts_f32x4 ts_mfma16x16x32(ts_u32x4 a, ts_u32x4 b, ts_f32x4 c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(ts_bf16x8, a),
+                                                   __builtin_bit_cast(ts_bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(ts_f16x8, a),
+                                                  __builtin_bit_cast(ts_f16x8, b), c, 0, 0, 0);
+}
+
+// D[32x32] += A[32x16] * B[16x32]. Lane l holds A row l%32, B column l%32,
+// k = 8*(l/32) + i, and D[8*(i/4) + 4*(l/32) + i%4][l%32] (checked on gfx950).
+template <bool BF16>
+TS_DEV ts_f32x16 ts_mfma32x32x16(ts_u32x4 a, ts_u32x4 b, ts_f32x16 c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(ts_bf16x8, a),
+                                                   __builtin_bit_cast(ts_bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(ts_f16x8, a),
+                                                  __builtin_bit_cast(ts_f16x8, b), c, 0, 0, 0);
+}
+
+// Non-temporal-free plain 16-byte global load (compiles to global_load_dwordx4).
+TS_DEV ts_u32x4 ts_ld16(const void* p) { return *reinterpret_cast<const ts_u32x4*>(p); }
+TS_DEV ts_u32x2 ts_ld8(const void* p) { return *reinterpret_cast<const ts_u32x2*>(p); }
+TS_DEV uint32_t ts_ld4(const void* p) { return *reinterpret_cast<const uint32_t*>(p); }
+
+// Host-side helpers shared by the entry points.
+#define TS_CHECK_LAUNCH()                                   \
+  do {                                                      \
+    if (hipGetLastError() != hipSuccess) return TS_HIP_ERROR; \
+  } while (0)
+
+__host__ __device__ inline int64_t ts_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -1,0 +1,105 @@
+"""GPU quantize entry points of the reference's gpu_quantize.py.
+
+``quantize_tensor_gpu`` (gpu_quantize.py:52-166) is the uniform-grid,
+no-double-quant GOAP flavour; here it is the same GPU codec as
+``codec.quantize_tensor`` with those options, so its codes, outlier order and
+metadata equal the reference CPU codec's bit for bit (the reference's own GPU
+path takes its outlier order from CUDA top-k). ``quantize_module_gpu``
+(gpu_quantize.py:212-386) quantizes layer by layer on the GPU.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from .codec import (
+    DEFAULT_ERROR_THRESHOLD,
+    DEFAULT_GROUP_SIZE,
+    DEFAULT_OUTLIER_FRAC,
+    QuantizedTensor,
+    quantize_tensor,
+    relative_error,
+)
+
+
+def quantize_tensor_gpu(w: torch.Tensor, bits: int = 4, group_size: int = DEFAULT_GROUP_SIZE,
+                        outlier_frac: float = DEFAULT_OUTLIER_FRAC) -> QuantizedTensor:
+    if bits not in (2, 4, 8):
+        raise ValueError("bits must be 2, 4, or 8")
+    if w.dim() == 1:
+        raise ValueError("quantize_tensor_gpu expects ndim >= 2")
+    return quantize_tensor(w, bits=bits, group_size=group_size, outlier_frac=outlier_frac)
+
+
+def quantize_tensor_gpu_adaptive(w: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE,
+                                 outlier_frac: float = DEFAULT_OUTLIER_FRAC,
+                                 error_threshold: float = DEFAULT_ERROR_THRESHOLD,
+                                 force_bits: Optional[int] = None) -> Tuple[QuantizedTensor, float, bool]:
+    """2 -> 4 -> 8 escalation (gpu_quantize.py:169-209)."""
+    if force_bits is not None:
+        qt = quantize_tensor_gpu(w, bits=force_bits, group_size=group_size, outlier_frac=outlier_frac)
+        return qt, relative_error(w, qt), False
+    for i, bits in enumerate((2, 4, 8)):
+        qt = quantize_tensor_gpu(w, bits=bits, group_size=group_size, outlier_frac=outlier_frac)
+        err = relative_error(w, qt)
+        if err <= error_threshold or bits == 8:
+            return qt, err, i > 0
+    raise AssertionError("unreachable")
+
+
+def quantize_module_gpu(model: torch.nn.Module, device: str = "cuda", bits: int = 4, group_size: int = 128,
+                        outlier_frac: float = 0.001, adaptive: bool = False, error_threshold: float = 0.10,
+                        min_numel: int = 16384,
+                        skip_name_patterns=("norm", "ln_", "embed", "lm_head", "shared", "position"),
+                        max_dequant_rows=4096, force_fp32_patterns=(), cache_budget_mb: float = 0.0,
+                        host_cache_budget_mb: float = 0.0, fast_dequant: bool = True, use_triton: bool = True,
+                        vram_budget_mb: Optional[float] = None, quantize_workers: Optional[int] = None,
+                        verbose: bool = True) -> dict:
+    """Uniform, no-double-quant layers quantized on the GPU (gpu_quantize.py:212-386)."""
+    from .codec import LayerBitStats, budget_allocate_bits, estimate_resident_nbytes
+    from .modules import QuantLinear, _iter_target_linears, _set_module_by_name
+    if cache_budget_mb > 0 or host_cache_budget_mb > 0:
+        raise NotImplementedError("WeightCache is not part of the tensorshrink_amd path")
+    fp32_pats = tuple(p.lower() for p in force_fp32_patterns)
+    targets = list(_iter_target_linears(model, min_numel, tuple(skip_name_patterns)))
+    stats = {"n_replaced": 0, "orig_bytes": 0, "packed_bytes": 0, "layers": [], "cache": None}
+    dev = torch.device(device)
+    plan = {}
+    if vram_budget_mb is not None:
+        ls = []
+        for name, lin in targets:
+            wg = lin.weight.data.to(dev)
+            q4 = quantize_tensor_gpu(wg, 4, group_size, outlier_frac)
+            q8 = quantize_tensor_gpu(wg, 8, group_size, outlier_frac)
+            ls.append(LayerBitStats(name, estimate_resident_nbytes(q4), estimate_resident_nbytes(q8),
+                                    relative_error(lin.weight.data, q4), relative_error(lin.weight.data, q8)))
+        plan = budget_allocate_bits(ls, vram_budget_mb * 1024 * 1024)
+    for name, lin in targets:
+        w = lin.weight.data
+        wg = w.to(dev)
+        f32 = any(p in name.lower() for p in fp32_pats)
+        if vram_budget_mb is not None:
+            qt = quantize_tensor_gpu(wg, plan[name], group_size, outlier_frac)
+            err, esc = relative_error(w, qt), plan[name] == 8
+        elif adaptive:
+            qt, err, esc = quantize_tensor_gpu_adaptive(wg, group_size, outlier_frac, error_threshold)
+        else:
+            qt = quantize_tensor_gpu(wg, bits, group_size, outlier_frac)
+            err, esc = relative_error(w, qt), False
+        bias = lin.bias.data if lin.bias is not None else None
+        qlin = QuantLinear(qt, bias, max_dequant_rows=max_dequant_rows, force_fp32_compute=f32,
+                           device=w.device if w.is_cuda else dev)
+        _set_module_by_name(model, name, qlin)
+        ob, pb = qlin.dense_equiv_nbytes(itemsize=w.element_size()), qlin.packed_nbytes()
+        stats["n_replaced"] += 1
+        stats["orig_bytes"] += ob
+        stats["packed_bytes"] += pb
+        stats["layers"].append(dict(name=name, bits=qlin.bits, rel_error=err, escalated=esc, orig_bytes=ob,
+                                    packed_bytes=pb, force_fp32_compute=f32))
+        if verbose:
+            print(f"  [{qlin.bits}b{'*' if esc else ' '}{' fp32' if f32 else ''}] {name:60s} err={err:.4f} "
+                  f"{ob / 1e6:8.3f}MB -> {pb / 1e6:8.3f}MB")
+    stats["ratio"] = stats["orig_bytes"] / max(1, stats["packed_bytes"]) if stats["orig_bytes"] > 0 else 1.0
+    stats["vram_budget_mb"] = vram_budget_mb
+    return stats

@@ -1,0 +1,424 @@
+"""QuantLinear and quantize_module on the MI355X kernels.
+
+Drop-in for modules.py of GDNickk/tensorshrink v0.4.0: ``QuantLinear``
+(modules.py:282-1026) registers the same buffers with the same names, dtypes
+and contents (packed, scale/gmin or dq_*, codebook, outlier_row/col sorted by
+row, outlier_delta, bias), and ``quantize_module`` (modules.py:1258-1455) takes
+the same arguments. The forward runs one libtensorshrink_hip launch per call
+(decode kernel for M <= 16, MFMA prefill kernel above), with the outlier
+correction and bias fused; there is no CPU or PyTorch fallback path.
+
+Additions over the reference:
+  * ``outlier_row_ptr`` - non-persistent int32 [rows + 1] CSR offsets into the
+    row-sorted outlier tables (derived data, absent from state_dict);
+  * 6-bit RVQ layers register ``stage2_packed``, ``stage2_scale`` and
+    ``stage2_gmin`` (the reference QuantLinear cannot serve bits=6).
+``WeightCache`` (a dense-weight cache) is not part of this path: passing
+``cache=`` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Iterable, Optional, Tuple, Union
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from . import _lib as L
+from .codec import (
+    DEFAULT_DQ_GROUP_SIZE,
+    LayerBitStats,
+    QuantizedTensor,
+    budget_allocate_bits,
+    estimate_resident_nbytes as _estimate_resident_nbytes,
+    quantize_tensor,
+    quantize_tensor_adaptive,
+    relative_error,
+)
+
+DEFAULT_SKIP_PATTERNS = ("norm", "ln_", "embed", "lm_head", "shared", "position")
+DEFAULT_MIN_NUMEL = 16384
+DEFAULT_MAX_DEQUANT_ROWS = 4096
+T5_EXTRA_SKIP_PATTERNS = (".wo",)
+
+
+class QuantLinear(nn.Module):
+    """nn.Linear replacement backed by packed 2/4/6/8-bit GOAP weights."""
+
+    def __init__(self, qt: QuantizedTensor, bias: Optional[torch.Tensor] = None,
+                 max_dequant_rows: Union[int, str] = DEFAULT_MAX_DEQUANT_ROWS, force_fp32_compute: bool = False,
+                 cache=None, fast_dequant: bool = True, use_triton: bool = True,
+                 device: Optional[torch.device] = None):
+        super().__init__()
+        if len(qt.orig_shape) != 2:
+            raise ValueError("QuantLinear requires a 2D weight (out_features, in_features)")
+        if cache is not None:
+            raise NotImplementedError("WeightCache is not part of the tensorshrink_amd path")
+        if qt.smooth_scale is not None:
+            raise NotImplementedError("smooth-scaled tensors are not covered by tensorshrink_amd")
+        self.out_features, self.in_features = qt.orig_shape
+        self.bits = qt.bits
+        self.group_size = qt.group_size
+        self.rows, self.cols = qt.rows, qt.cols
+        self.padded_cols = qt.padded_cols
+        self.n_groups = qt.n_groups
+        self.orig_dtype_str = qt.orig_dtype
+        self.max_dequant_rows = DEFAULT_MAX_DEQUANT_ROWS if max_dequant_rows == "auto" else max(1, int(max_dequant_rows))
+        self.cache = None
+        self.fast_dequant = fast_dequant
+        self.use_triton = use_triton
+        self.force_fp32_compute = force_fp32_compute
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device()) \
+            if torch.cuda.is_available() else None
+        if dev is None or dev.type != "cuda":
+            L.lib()  # raises: no GPU
+        lib = L.lib()
+
+        def t(a, dtype=None):
+            x = torch.from_numpy(np.ascontiguousarray(a))
+            return (x.to(dtype) if dtype is not None else x).to(dev)
+
+        self.register_buffer("packed", t(qt.packed))
+        self.double_quant = qt.dq_scale_codes is not None
+        if self.double_quant:
+            self.dq_group_size = int(qt.dq_scale_codes.shape[0] // qt.dq_scale_meta.shape[0])
+            self.register_buffer("dq_scale_codes", t(qt.dq_scale_codes))
+            self.register_buffer("dq_scale_meta", t(qt.dq_scale_meta))
+            self.register_buffer("dq_gmin_codes", t(qt.dq_gmin_codes))
+            self.register_buffer("dq_gmin_meta", t(qt.dq_gmin_meta))
+            self.scale = None
+            self.gmin = None
+        else:
+            self.dq_group_size = 0
+            self.register_buffer("scale", t(qt.scale))
+            self.register_buffer("gmin", t(qt.gmin))
+        self.companded = qt.codebook is not None
+        if self.companded:
+            self.register_buffer("codebook", t(qt.codebook, torch.float32))
+        else:
+            self.codebook = None
+        if qt.bits == 6:
+            self.register_buffer("stage2_packed", t(qt.stage2_packed))
+            self.register_buffer("stage2_scale", t(qt.stage2_scale))
+            self.register_buffer("stage2_gmin", t(qt.stage2_gmin))
+
+        # Outlier tables (modules.py:414-448) built on the GPU: stable row
+        # sort, delta = f16(val - base) with QuantLinear's float32 scale/gmin.
+        n = qt.n_outliers()
+        orow = torch.empty(n, dtype=torch.int32, device=dev)
+        ocol = torch.empty(n, dtype=torch.int32, device=dev)
+        odelta = torch.empty(n, dtype=torch.float16, device=dev)
+        rptr = torch.empty(self.rows + 1, dtype=torch.int32, device=dev)
+        idx = t(np.ascontiguousarray(qt.outlier_idx, dtype=np.int32))
+        val = t(np.ascontiguousarray(qt.outlier_val, dtype=np.float16))
+        layer = self._make_layer(with_outliers=False)
+        ws_n = lib.ts_outlier_tables_workspace_bytes(n, self.rows)
+        ws = torch.empty(max(1, ws_n), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            L.check(lib.ts_build_outlier_tables(ctypes.byref(layer), idx.data_ptr(), val.data_ptr(), n,
+                                                orow.data_ptr(), ocol.data_ptr(), odelta.data_ptr(),
+                                                rptr.data_ptr(), ws.data_ptr(), ws.numel(), L.stream_ptr(dev)),
+                    "outlier tables")
+        self.register_buffer("outlier_row", orow)
+        self.register_buffer("outlier_col", ocol)
+        self.register_buffer("outlier_delta", odelta)
+        self.register_buffer("outlier_row_ptr", rptr, persistent=False)
+        if bias is not None:
+            self.register_buffer("bias", bias.detach().clone().to(dev))
+        else:
+            self.bias = None
+        self._layer = None
+        self._bias_cache = {}
+        self._rebuild_cache()
+
+    # -- kernel view -----------------------------------------------------
+    def _make_layer(self, with_outliers: bool = True) -> L.QLayer:
+        s = L.QLayer()
+        s.bits, s.group_size = self.bits, self.group_size
+        s.rows, s.cols, s.padded_cols, s.n_groups = self.rows, self.cols, self.padded_cols, self.n_groups
+        s.packed = self.packed.data_ptr()
+        s.packed_stride = self.packed.shape[1]
+        if self.double_quant:
+            s.dq_scale_codes = self.dq_scale_codes.data_ptr()
+            s.dq_scale_meta = self.dq_scale_meta.data_ptr()
+            s.dq_gmin_codes = self.dq_gmin_codes.data_ptr()
+            s.dq_gmin_meta = self.dq_gmin_meta.data_ptr()
+            s.dq_group_size = self.dq_group_size
+        else:
+            s.scale = self.scale.data_ptr()
+            s.gmin = self.gmin.data_ptr()
+        if self.companded:
+            s.codebook = self.codebook.data_ptr()
+        if self.bits == 6:
+            s.stage2_packed = self.stage2_packed.data_ptr()
+            s.stage2_stride = self.stage2_packed.shape[1]
+            s.stage2_scale = self.stage2_scale.data_ptr()
+            s.stage2_gmin = self.stage2_gmin.data_ptr()
+        if with_outliers and self.outlier_row.numel() > 0:
+            s.outlier_row = self.outlier_row.data_ptr()
+            s.outlier_col = self.outlier_col.data_ptr()
+            s.outlier_delta = self.outlier_delta.data_ptr()
+            s.n_outliers = self.outlier_row.numel()
+            s.outlier_row_ptr = self.outlier_row_ptr.data_ptr()
+        return s
+
+    def _rebuild_cache(self) -> None:
+        self._layer = self._make_layer() if self.packed.is_cuda else None
+        self._bias_cache = {}
+
+    def _apply(self, fn, recurse=True):
+        result = super()._apply(fn, recurse=recurse)
+        self._rebuild_cache()
+        return result
+
+    # -- introspection (modules.py:527-593) ------------------------------
+    @property
+    def weight(self) -> torch.Tensor:
+        return torch.empty(self.out_features, self.in_features, dtype=torch.int8, device="meta")
+
+    def packed_nbytes(self) -> int:
+        n = self.packed.numel() * self.packed.element_size()
+        if self.double_quant:
+            for b in (self.dq_scale_codes, self.dq_scale_meta, self.dq_gmin_codes, self.dq_gmin_meta):
+                n += b.numel() * b.element_size()
+        else:
+            n += self.scale.numel() * self.scale.element_size() + self.gmin.numel() * self.gmin.element_size()
+        if self.bits == 6:
+            for b in (self.stage2_packed, self.stage2_scale, self.stage2_gmin):
+                n += b.numel() * b.element_size()
+        for b in (self.outlier_row, self.outlier_col, self.outlier_delta):
+            n += b.numel() * b.element_size()
+        return n
+
+    @staticmethod
+    def estimate_resident_nbytes(qt: QuantizedTensor) -> int:
+        return _estimate_resident_nbytes(qt)
+
+    def dense_equiv_nbytes(self, itemsize: int = 2) -> int:
+        return self.out_features * self.in_features * itemsize
+
+    def dequantize_weight(self, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """Dense W [out, in] as this layer computes with it (outliers = base + delta)."""
+        w = torch.empty(self.rows, self.cols, dtype=dtype, device=self.packed.device)
+        L.check(L.lib().ts_dequantize(ctypes.byref(self._layer), L.TS_DEQ_QLINEAR, None, None, 0, w.data_ptr(),
+                                      self.cols, L.dtype_code(dtype), L.stream_ptr(self.packed.device)),
+                "dequantize")
+        return w
+
+    def to_quantized_tensor(self) -> QuantizedTensor:
+        """Rebuild a QuantizedTensor (modules.py:595-645); outlier_val = f16(base + delta)."""
+        row = self.outlier_row.cpu().numpy().astype(np.int64)
+        col = self.outlier_col.cpu().numpy().astype(np.int64)
+        idx = (row * self.cols + col).astype(np.int32)
+        w = self.dequantize_weight(torch.float32)
+        oval = w.reshape(-1)[torch.from_numpy(idx.astype(np.int64)).to(w.device)].to(torch.float16).cpu().numpy() \
+            if idx.size else np.zeros(0, np.float16)
+        kw = dict(orig_shape=(self.out_features, self.in_features), orig_dtype=self.orig_dtype_str, bits=self.bits,
+                  group_size=self.group_size, rows=self.rows, cols=self.cols, padded_cols=self.padded_cols,
+                  n_groups=self.n_groups, packed=self.packed.cpu().numpy(), outlier_idx=idx, outlier_val=oval)
+        if self.double_quant:
+            kw.update(dq_scale_codes=self.dq_scale_codes.cpu().numpy(), dq_scale_meta=self.dq_scale_meta.cpu().numpy(),
+                      dq_gmin_codes=self.dq_gmin_codes.cpu().numpy(), dq_gmin_meta=self.dq_gmin_meta.cpu().numpy())
+            sc = self.dq_scale_codes.cpu().numpy().astype(np.float32).reshape(self.dq_scale_meta.shape[0], -1)
+            gc = self.dq_gmin_codes.cpu().numpy().astype(np.float32).reshape(self.dq_gmin_meta.shape[0], -1)
+            sm = self.dq_scale_meta.cpu().numpy().astype(np.float32)
+            gm = self.dq_gmin_meta.cpu().numpy().astype(np.float32)
+            n = self.rows * self.n_groups
+            kw["scale"] = (sc * sm[:, :1] + sm[:, 1:]).ravel()[:n].reshape(self.rows, self.n_groups).astype(np.float16)
+            kw["gmin"] = (gc * gm[:, :1] + gm[:, 1:]).ravel()[:n].reshape(self.rows, self.n_groups).astype(np.float16)
+        else:
+            kw.update(scale=self.scale.cpu().numpy(), gmin=self.gmin.cpu().numpy())
+        if self.companded:
+            kw["codebook"] = self.codebook.cpu().numpy()
+        if self.bits == 6:
+            kw.update(stage2_packed=self.stage2_packed.cpu().numpy(), stage2_scale=self.stage2_scale.cpu().numpy(),
+                      stage2_gmin=self.stage2_gmin.cpu().numpy())
+        return QuantizedTensor(**kw)
+
+    # -- forward (modules.py:819-940) -------------------------------------
+    def _bias_as(self, dtype: torch.dtype) -> Optional[torch.Tensor]:
+        if self.bias is None:
+            return None
+        b = self._bias_cache.get(dtype)
+        if b is None:
+            b = self.bias.to(dtype).contiguous()
+            self._bias_cache[dtype] = b
+        return b
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._layer is None or not x.is_cuda:
+            raise RuntimeError("QuantLinear.forward runs on the GPU kernels only: move the module and the input "
+                               "to a ROCm device")
+        in_dtype = x.dtype
+        M = 1
+        for d in x.shape[:-1]:
+            M *= d
+        lead = x.shape[:-1]
+        x2d = x.reshape(M, self.in_features)
+        if self.force_fp32_compute or in_dtype == torch.float32:
+            # fp32 compute: GPU dequant (QuantLinear view) + a plain library GEMM.
+            w = self.dequantize_weight(torch.float32)
+            b = self._bias_as(torch.float32)
+            y = torch.nn.functional.linear(x2d.to(torch.float32), w, b)
+            return y.to(in_dtype).reshape(*lead, self.out_features)
+        if in_dtype not in (torch.float16, torch.bfloat16):
+            raise TypeError(f"unsupported activation dtype {in_dtype}")
+        if not x2d.is_contiguous():
+            x2d = x2d.contiguous()
+        y = torch.empty(M, self.out_features, dtype=in_dtype, device=x.device)
+        b = self._bias_as(in_dtype)
+        dt = L.dtype_code(in_dtype)
+        L.check(L.load().ts_qlinear_forward(ctypes.byref(self._layer), x2d.data_ptr(), M, self.in_features, dt,
+                                            y.data_ptr(), self.out_features, dt, L.ptr(b), None, 0,
+                                            L.stream_ptr(x.device)), "qlinear forward")
+        return y.reshape(*lead, self.out_features)
+
+    @classmethod
+    def from_linear(cls, linear: nn.Linear, bits: int = 4, group_size: int = 128, outlier_frac: float = 0.001,
+                    adaptive: bool = False, error_threshold: float = 0.10,
+                    max_dequant_rows: Union[int, str] = DEFAULT_MAX_DEQUANT_ROWS, force_fp32_compute: bool = False,
+                    cache=None, fast_dequant: bool = True, use_triton: bool = True, companded: bool = False,
+                    double_quant: bool = True, dq_group_size: int = DEFAULT_DQ_GROUP_SIZE,
+                    nf_quant: bool = True) -> Tuple["QuantLinear", float, bool]:
+        """modules.py:942-1003."""
+        w = linear.weight.data
+        if adaptive:
+            qt, err, escalated = quantize_tensor_adaptive(
+                w, group_size=group_size, outlier_frac=outlier_frac, error_threshold=error_threshold,
+                allowed_bits=(2, 4, 8), companded=companded, double_quant=double_quant,
+                dq_group_size=dq_group_size, nf_quant=nf_quant)
+        else:
+            qt = quantize_tensor(w, bits=bits, group_size=group_size, outlier_frac=outlier_frac, companded=companded,
+                                 double_quant=double_quant, dq_group_size=dq_group_size, nf_quant=nf_quant)
+            err = relative_error(w, qt)
+            escalated = False
+        bias = linear.bias.data if linear.bias is not None else None
+        dev = linear.weight.device if linear.weight.is_cuda else None
+        qlin = cls(qt, bias, max_dequant_rows=max_dequant_rows, force_fp32_compute=force_fp32_compute, cache=cache,
+                   fast_dequant=fast_dequant, use_triton=use_triton, device=dev)
+        return qlin, err, escalated
+
+    @classmethod
+    def from_quantized_tensor(cls, qt: QuantizedTensor, bias: Optional[torch.Tensor] = None,
+                              max_dequant_rows: Union[int, str] = DEFAULT_MAX_DEQUANT_ROWS,
+                              force_fp32_compute: bool = False, cache=None, fast_dequant: bool = True,
+                              use_triton: bool = True) -> "QuantLinear":
+        return cls(qt, bias, max_dequant_rows=max_dequant_rows, force_fp32_compute=force_fp32_compute, cache=cache,
+                   fast_dequant=fast_dequant, use_triton=use_triton)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, bits={self.bits}, "
+                f"group_size={self.group_size}, packed_kB={self.packed_nbytes() / 1024:.1f}, "
+                f"dense_fp16_kB={self.dense_equiv_nbytes() / 1024:.1f}")
+
+
+# ---------------------------------------------------------------------------
+# whole-model helpers (modules.py:1033-1455)
+# ---------------------------------------------------------------------------
+
+def _set_module_by_name(root: nn.Module, dotted: str, new: nn.Module) -> None:
+    parts = dotted.split(".")
+    obj = root
+    for p in parts[:-1]:
+        obj = getattr(obj, p)
+    setattr(obj, parts[-1], new)
+
+
+def _iter_target_linears(model: nn.Module, min_numel: int, skip_name_patterns: Iterable[str]):
+    pats = tuple(p.lower() for p in skip_name_patterns)
+    for name, module in model.named_modules():
+        if isinstance(module, nn.Linear) and not isinstance(module, QuantLinear):
+            if module.weight.numel() < min_numel:
+                continue
+            if any(p in name.lower() for p in pats):
+                continue
+            yield name, module
+
+
+def model_weight_bytes(model: nn.Module) -> int:
+    return sum(p.numel() * p.element_size() for p in model.parameters()) + \
+        sum(b.numel() * b.element_size() for b in model.buffers())
+
+
+def quantize_module(
+    model: nn.Module,
+    bits: int = 4,
+    group_size: int = 128,
+    outlier_frac: float = 0.001,
+    adaptive: bool = False,
+    error_threshold: float = 0.10,
+    min_numel: int = DEFAULT_MIN_NUMEL,
+    skip_name_patterns: Iterable[str] = DEFAULT_SKIP_PATTERNS,
+    max_dequant_rows: Union[int, str] = DEFAULT_MAX_DEQUANT_ROWS,
+    force_fp32_patterns: Iterable[str] = (),
+    cache_budget_mb: float = 0.0,
+    host_cache_budget_mb: float = 0.0,
+    fast_dequant: bool = True,
+    use_triton: bool = True,
+    vram_budget_mb: Optional[float] = None,
+    quantize_workers: Optional[int] = 4,
+    verbose: bool = True,
+    companded: bool = False,
+    double_quant: bool = True,
+    dq_group_size: int = DEFAULT_DQ_GROUP_SIZE,
+    nf_quant: bool = True,
+) -> dict:
+    """Replace every eligible nn.Linear with a QuantLinear, in place
+    (modules.py:1258-1455). Layers are quantized on the GPU one after another;
+    `quantize_workers` is accepted for signature compatibility."""
+    if cache_budget_mb > 0 or host_cache_budget_mb > 0:
+        raise NotImplementedError("WeightCache is not part of the tensorshrink_amd path")
+    targets = list(_iter_target_linears(model, min_numel, skip_name_patterns))
+    fp32_pats = tuple(p.lower() for p in force_fp32_patterns)
+    stats = {"n_replaced": 0, "orig_bytes": 0, "packed_bytes": 0, "layers": [], "cache": None}
+
+    def record(name, qlin, err, escalated, force_fp32, itemsize):
+        ob = qlin.dense_equiv_nbytes(itemsize=itemsize)
+        pb = qlin.packed_nbytes()
+        stats["n_replaced"] += 1
+        stats["orig_bytes"] += ob
+        stats["packed_bytes"] += pb
+        stats["layers"].append(dict(name=name, bits=qlin.bits, rel_error=err, escalated=escalated, orig_bytes=ob,
+                                    packed_bytes=pb, force_fp32_compute=force_fp32))
+        if verbose:
+            print(f"  [{qlin.bits}b{'*' if escalated else ' '}{' fp32' if force_fp32 else ''}] {name:60s} "
+                  f"err={err:.4f} {ob / 1e6:8.3f}MB -> {pb / 1e6:8.3f}MB")
+
+    if vram_budget_mb is not None:
+        if companded:
+            raise ValueError("companded=True is not yet supported with vram_budget_mb (budget-aware path)")
+        computed, lstats = {}, []
+        for name, lin in targets:
+            w = lin.weight.data
+            q4 = quantize_tensor(w, bits=4, group_size=group_size, outlier_frac=outlier_frac)
+            q8 = quantize_tensor(w, bits=8, group_size=group_size, outlier_frac=outlier_frac)
+            e4, e8 = relative_error(w, q4), relative_error(w, q8)
+            lstats.append(LayerBitStats(name, _estimate_resident_nbytes(q4), _estimate_resident_nbytes(q8), e4, e8))
+            computed[name] = {4: (q4, e4), 8: (q8, e8)}
+        plan = budget_allocate_bits(lstats, vram_budget_mb * 1024 * 1024)
+        for name, lin in targets:
+            qt, err = computed[name][plan[name]]
+            f32 = any(p in name.lower() for p in fp32_pats)
+            bias = lin.bias.data if lin.bias is not None else None
+            qlin = QuantLinear(qt, bias, max_dequant_rows=max_dequant_rows, force_fp32_compute=f32,
+                               device=lin.weight.device if lin.weight.is_cuda else None)
+            _set_module_by_name(model, name, qlin)
+            record(name, qlin, err, plan[name] == 8, f32, lin.weight.element_size())
+        stats["ratio"] = stats["orig_bytes"] / max(1, stats["packed_bytes"]) if stats["orig_bytes"] else 1.0
+        stats["vram_budget_mb"] = vram_budget_mb
+        stats["budget_bytes_used"] = stats["packed_bytes"]
+        return stats
+
+    for i, (name, lin) in enumerate(targets):
+        f32 = any(p in name.lower() for p in fp32_pats)
+        qlin, err, esc = QuantLinear.from_linear(
+            lin, bits=bits, group_size=group_size, outlier_frac=outlier_frac, adaptive=adaptive,
+            error_threshold=error_threshold, max_dequant_rows=max_dequant_rows, force_fp32_compute=f32,
+            fast_dequant=fast_dequant, use_triton=use_triton, companded=companded, double_quant=double_quant,
+            dq_group_size=dq_group_size, nf_quant=nf_quant)
+        _set_module_by_name(model, name, qlin)
+        targets[i] = None
+        record(name, qlin, err, esc, f32, lin.weight.element_size())
+    stats["ratio"] = stats["orig_bytes"] / max(1, stats["packed_bytes"]) if stats["orig_bytes"] > 0 else 1.0
+    return stats

@@ -1,0 +1,155 @@
+"""QuantLinear forward on the decode (M <= 16) and prefill (M > 16) kernels:
+max |y - y_ref| / max |y_ref| <= 1e-2 against the reference's
+dequantize-then-matmul in float32/float64."""
+import numpy as np
+import pytest
+import torch
+
+import recipes
+from golden_io import case_names, load_case, qopts
+from gpu_util import max_rel_err, qt_from_golden, say, weight_for
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2  # max relative error, fp32 accumulation
+
+
+def _ts():
+    import tensorshrink_amd as ts
+    return ts
+
+
+@pytest.mark.parametrize("name", case_names())
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 64, 300])
+def test_forward_small_cases(name, M):
+    spec, res, d, w = load_case(name)
+    ts = _ts()
+    say("forward", name, M)
+    bias = torch.from_numpy(d["ql_bias"]).view(w.dtype) if "ql_bias" in d.files else None
+    ql = ts.QuantLinear(qt_from_golden(d, res), bias)
+    x = recipes.activations(M, res["meta"]["cols"], seed=100 + M)
+    y = ql(x.cuda())
+    assert y.dtype == torch.bfloat16 and y.shape == (M, res["meta"]["rows"])
+    W = torch.from_numpy(d["deq_f32"]).double()
+    y_ref = x.double() @ W.T
+    if bias is not None:
+        y_ref += bias.double()
+    err = max_rel_err(y.cpu(), y_ref)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 40])
+def test_forward_fp16_activations(M):
+    spec, res, d, w = load_case("nf4_dq_g128")
+    ql = _ts().QuantLinear(qt_from_golden(d, res))
+    x = recipes.activations(M, res["meta"]["cols"], seed=5, dtype=torch.float16)
+    y = ql(x.cuda())
+    assert y.dtype == torch.float16
+    y_ref = x.double() @ torch.from_numpy(d["deq_f32"]).double().T
+    assert max_rel_err(y.cpu(), y_ref) <= TOL
+
+
+def test_forward_fp32_and_3d_input():
+    spec, res, d, w = load_case("u4_dq_g128_bias")
+    bias = torch.from_numpy(d["ql_bias"]).view(w.dtype)
+    ql = _ts().QuantLinear(qt_from_golden(d, res), bias)
+    x = recipes.activations(6, res["meta"]["cols"], seed=9).float().reshape(2, 3, -1)
+    y = ql(x.cuda())
+    assert y.shape == (2, 3, res["meta"]["rows"]) and y.dtype == torch.float32
+    y_ref = x.double().reshape(6, -1) @ torch.from_numpy(d["deq_f32"]).double().T + bias.double()
+    assert max_rel_err(y.cpu().reshape(6, -1), y_ref) <= TOL
+
+
+def _layer(rows, cols, seed, opts, sigma=0.02):
+    ts = _ts()
+    w = recipes.gaussian_weight(rows, cols, seed, sigma=sigma)
+    qt = ts.quantize_tensor(w, **opts)
+    W = ts.dequantize_tensor(qt, device="cuda", dtype=torch.float32)
+    return ts.QuantLinear(qt), W
+
+
+NF4 = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("M", [1, 16])
+def test_cfg1_4096_nf4(M):
+    ql, W = _layer(4096, 4096, 1000, NF4)
+    x = recipes.activations(M, 4096).cuda()
+    err = max_rel_err(ql(x).float(), x.float() @ W.T)
+    say("cfg1 M", M, "err", err)
+    assert err <= TOL
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_cfg2_11008_lm2(M):
+    ts = _ts()
+    w = recipes.student_t_weight(11008, 4096, 2000)
+    torch.manual_seed(2024)
+    qt = ts.quantize_tensor(w, bits=2, group_size=64, outlier_frac=0.001, double_quant=True, companded=True)
+    W = ts.dequantize_tensor(qt, device="cuda", dtype=torch.float32)
+    ql = ts.QuantLinear(qt)
+    x = recipes.activations(M, 4096).cuda()
+    err = max_rel_err(ql(x).float(), x.float() @ W.T)
+    say("cfg2 M", M, "err", err)
+    assert err <= TOL
+
+
+@pytest.mark.slow
+def test_cfg3_llama8b_layer():
+    for i, (name, n, k) in enumerate(recipes.LLAMA3_8B_LINEARS):
+        ql, W = _layer(n, k, recipes.layer_seed(i), NF4)
+        for M in (1, 4, 16):
+            x = recipes.activations(M, k).cuda()
+            err = max_rel_err(ql(x).float(), x.float() @ W.T)
+            say("cfg3", name, M, err)
+            assert err <= TOL, (name, M, err)
+        del ql, W
+        torch.cuda.empty_cache()
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("bits", [8, 6])
+def test_cfg4_prefill_2048(bits):
+    opts = dict(bits=bits, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+    x = recipes.activations(2048, 4096).cuda()
+    for i, (name, n, k) in enumerate(recipes.LLAMA3_8B_LINEARS[4:6]):
+        ql, W = _layer(n, k, recipes.layer_seed(4 + i), opts)
+        err = max_rel_err(ql(x).float(), x.float() @ W.T)
+        say("cfg4", bits, name, err)
+        assert err <= TOL
+    name, n, k = recipes.LLAMA3_8B_LINEARS[6]
+    ql, W = _layer(n, k, recipes.layer_seed(6), opts)
+    x2 = recipes.activations(2048, k).cuda()
+    err = max_rel_err(ql(x2).float(), x2.float() @ W.T)
+    say("cfg4", bits, name, err)
+    assert err <= TOL
+
+
+def test_kernel_api_functions():
+    ts = _ts()
+    spec, res, d, w = load_case("u4_dq_g128_bias")
+    ql = ts.QuantLinear(qt_from_golden(d, res))
+    x = recipes.activations(5, res["meta"]["cols"], seed=3).cuda()
+    y = ts.fused_quantized_linear(x, ql.packed, None, None, None, 4, 128, ql.cols, ql.out_features, torch.bfloat16,
+                                  return_fp32=True, outlier_row=ql.outlier_row, outlier_col=ql.outlier_col,
+                                  outlier_delta=ql.outlier_delta, dq_scale_codes=ql.dq_scale_codes,
+                                  dq_scale_meta=ql.dq_scale_meta, dq_gmin_codes=ql.dq_gmin_codes,
+                                  dq_gmin_meta=ql.dq_gmin_meta, dq_group_size=ql.dq_group_size,
+                                  n_groups=ql.n_groups)
+    W = torch.from_numpy(d["deq_f32"]).cuda()
+    assert y.dtype == torch.float32
+    assert max_rel_err(y, x.float() @ W.T) <= TOL
+    # uncorrected GEMM + standalone outlier pass == corrected GEMM
+    y0 = ts.fused_quantized_linear(x, ql.packed, None, None, None, 4, 128, ql.cols, ql.out_features, torch.bfloat16,
+                                   return_fp32=True, dq_scale_codes=ql.dq_scale_codes, dq_scale_meta=ql.dq_scale_meta,
+                                   dq_gmin_codes=ql.dq_gmin_codes, dq_gmin_meta=ql.dq_gmin_meta,
+                                   dq_group_size=ql.dq_group_size, n_groups=ql.n_groups)
+    y1 = ts.apply_outlier_correction(y0.clone(), x, ql.outlier_row, ql.outlier_col, ql.outlier_delta)
+    assert torch.allclose(y1, y, rtol=1e-5, atol=1e-5)
+    # dense dequant of the QuantLinear view equals the codec view off the outliers
+    Wq = ql.dequantize_weight(torch.float32)
+    mask = torch.ones(W.numel(), dtype=torch.bool, device="cuda")
+    mask[torch.from_numpy(d["qt_outlier_idx"].astype(np.int64)).cuda()] = False
+    assert torch.equal(Wq.reshape(-1)[mask], W.reshape(-1)[mask])

@@ -1,0 +1,117 @@
+"""The C-ABI library without a GPU: it loads, exports every declared symbol,
+and its host-side functions (exact top-k replay, Lloyd-Max fit) agree with the
+oracle. CPU only."""
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import recipes
+from oracle import codec_ref as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _lib():
+    from tensorshrink_amd import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.skip("libtensorshrink_hip.so not built")
+    return L, L.load()
+
+
+def test_exports_every_declared_symbol():
+    L, lib = _lib()
+    header = open(os.path.join(ROOT, "include", "tensorshrink_hip.h")).read()
+    names = set(re.findall(r"^\s*(?:const\s+char\s*\*|int|size_t)\s+(ts_\w+)\s*\(", header, re.M))
+    assert len(names) >= 20
+    for n in sorted(names):
+        assert hasattr(lib, n), n
+        assert n in L.PROTOTYPES, f"{n} has no ctypes prototype"
+
+
+def test_status_strings():
+    L, lib = _lib()
+    assert lib.ts_status_str(L.TS_OK) == b"ok"
+    assert b"covered" in lib.ts_status_str(L.TS_NOT_COVERED)
+    assert b"gfx950" in lib.ts_version()
+
+
+def _select(lib, cidx, cval, n, k):
+    oi = np.empty(k, np.int64)
+    ov = np.empty(k, np.float32)
+    cidx = np.ascontiguousarray(cidx, np.int64)
+    cval = np.ascontiguousarray(cval, np.float32)
+    rc = lib.ts_topk_select(cidx.ctypes.data, cval.ctypes.data, len(cidx), n, k, oi.ctypes.data, ov.ctypes.data)
+    return rc, oi, ov
+
+
+def _prefix_filter(a, k):
+    """The GPU candidate rule restated on the CPU: [0, k) plus, in segment
+    [k 2^(s-1), k 2^s), values above a lower bound of the k-th largest of the
+    preceding prefix (here: that exact value, the tightest valid bound)."""
+    n = a.shape[0]
+    keep = np.zeros(n, bool)
+    keep[:k] = True
+    start = k
+    while start < n:
+        end = min(2 * start, n)
+        kth = np.partition(a[:start], start - k)[start - k]
+        keep[start:end] = a[start:end] > kth
+        start = end
+    return keep
+
+
+@pytest.mark.parametrize("n,k,kind", [(200000, 200, "gauss"), (120000, 1500, "ties"), (65536, 1024, "ties"),
+                                      (5000, 600, "ties"), (5000, 4999, "gauss")])
+def test_topk_select_replay(n, k, kind):
+    L, lib = _lib()
+    g = torch.Generator().manual_seed(n ^ k)
+    if kind == "ties":
+        a = (torch.randint(-30, 31, (n,), generator=g).float() / 30).to(torch.float16).float().abs().numpy()
+    else:
+        a = torch.randn(n, generator=g).to(torch.float16).float().abs().numpy()
+    ov_ref, oi_ref = O.topk_abs(a, k)
+    rc, oi, ov = _select(lib, np.arange(n), a, n, k)
+    assert rc == 0
+    np.testing.assert_array_equal(oi, oi_ref)
+    np.testing.assert_array_equal(ov, ov_ref)
+    if k * 64 <= n:
+        keep = _prefix_filter(a, k)
+        assert keep.sum() < n
+        rc, oi2, ov2 = _select(lib, np.nonzero(keep)[0], a[keep], n, k)
+        assert rc == 0
+        np.testing.assert_array_equal(oi2, oi_ref)
+    else:
+        # the nth_element regime needs the whole array
+        rc, _, _ = _select(lib, np.arange(n - 1), a[:-1], n, k)
+        assert rc == L.TS_BAD_ARG
+
+
+def test_topk_select_rejects_bad_stream():
+    L, lib = _lib()
+    a = np.random.default_rng(1).random(10000).astype(np.float32)
+    rc, _, _ = _select(lib, np.arange(1, 10000), a[1:], 10000, 10)
+    assert rc == L.TS_BAD_ARG
+
+
+@pytest.mark.parametrize("levels,m", [(4, 30000), (16, 50000), (4, 7)])
+def test_lloyd_max_host_matches_oracle(levels, m):
+    L, lib = _lib()
+    rng = np.random.default_rng(levels + m)
+    x = (rng.standard_t(5, m) * 0.5 + 1.5).astype(np.float32)
+    nl = max(1, min(levels, m))
+    init = torch.linspace(float(x.min()), float(x.max()), nl).numpy()
+    out = np.empty(nl, np.float32)
+    assert lib.ts_lloyd_max_fit_host(x.ctypes.data, m, init.ctypes.data, nl, 12, out.ctypes.data) == 0
+    ref = O.lloyd_max_fit(x, levels, None)
+    np.testing.assert_array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_no_gpu_fails_loudly():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    import tensorshrink_amd as ts
+    with pytest.raises(RuntimeError, match="GPU"):
+        ts.quantize_tensor(recipes.gaussian_weight(8, 128, 0))
