@@ -1,0 +1,304 @@
+#!/usr/bin/env python
+"""Benchmark of the GOAP quantized-linear path on one MI355X.
+
+Metric: QuantLinear M=1 HBM GB/s (% of 8 TB/s peak) and
+M=2048 TFLOPS (% of the 2.5 PFLOP/s dense bf16 MFMA peak).
+
+Workload (`value`): decode at M=1 through the seven linears of a
+Llama-3-8B-shaped decoder layer (q 4096x4096, k/v 1024x4096, o 4096x4096,
+gate/up 14336x4096, down 4096x14336), 4-bit NF4 + double quant, group 128,
+0.1 % outliers (the 4-bit M=1 decode target). One step is
+one layer forward (7 QuantLinear calls, one kernel launch each). Ten copies of
+the layer (1.2 GB) are rotated so every step streams its weights from HBM and
+not from the 256 MB MALL; each copy's step is a captured HIP graph.
+
+Alongside it (extra keys of the same JSON line):
+  * "roofline"     - the decode kernel: algorithmic bytes of every launch in the
+                     timed region / their summed durations (HIP events around
+                     each launch, recorded inside the graphs), vs 8 TB/s;
+  * "prefill"      - BASELINE config 4: gate/up/down at M=2048, 8-bit NF8 + DQ
+                     and 6-bit RVQ, 2*M*N*K flops / kernel time vs 2.5 PFLOP/s;
+  * "cpu_baseline" - the reference CPU fallback forward (bf16 dequant + F.linear,
+                     modules.py:752-804, 924-940), restated in oracle/, timed
+                     on this host's cores for one layer forward at M=1.
+Synthetic seeded weights/activations (tests/golden/recipes.py).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def layer_bytes(ql, M: int) -> int:
+    """Algorithmic bytes of one decode launch: packed + metadata + outliers +
+    codebook + x + y (+ bias), as in the survey's measurement section."""
+    N, K = ql.out_features, ql.in_features
+    b = ql.packed.numel()
+    if ql.double_quant:
+        b += ql.dq_scale_codes.numel() + ql.dq_gmin_codes.numel()
+        b += (ql.dq_scale_meta.numel() + ql.dq_gmin_meta.numel()) * 2
+    else:
+        b += (ql.scale.numel() + ql.gmin.numel()) * 2
+    if ql.bits == 6:
+        b += ql.stage2_packed.numel() + (ql.stage2_scale.numel() + ql.stage2_gmin.numel()) * 2
+    b += ql.outlier_row.numel() * (4 + 4 + 2)
+    if ql.codebook is not None:
+        b += ql.codebook.numel() * 4
+    b += M * K * 2 + M * N * 2
+    if ql.bias is not None:
+        b += N * 2
+    return int(b)
+
+
+def clone_layer(ql):
+    """A second QuantLinear over fresh copies of the same buffers."""
+    import copy
+    c = copy.copy(ql)
+    c._buffers = {k: (v.clone() if v is not None else None) for k, v in ql._buffers.items()}
+    c._rebuild_cache()
+    return c
+
+
+def build_decode_layer(opts):
+    import recipes
+    import tensorshrink_amd as ts
+    layer = []
+    for i, (name, n, k) in enumerate(recipes.LLAMA3_8B_LINEARS):
+        w = recipes.gaussian_weight(n, k, recipes.layer_seed(i))
+        t0 = time.time()
+        qt = ts.quantize_tensor(w, **opts)
+        ql = ts.QuantLinear(qt)
+        log(f"  quantized {name} {n}x{k} in {time.time() - t0:.2f}s")
+        layer.append((name, ql))
+    return layer
+
+
+def bench_decode(args, opts):
+    import recipes
+    torch.cuda.synchronize()
+    base = build_decode_layer(opts)
+    copies = [base] + [[(n, clone_layer(q)) for n, q in base] for _ in range(args.copies - 1)]
+    xs = {4096: recipes.activations(1, 4096).cuda(), 14336: recipes.activations(1, 14336).cuda()}
+    step_bytes = sum(layer_bytes(q, 1) for _, q in base)
+    stream = torch.cuda.Stream()
+    graphs, events, outs = [], [], []
+    with torch.cuda.stream(stream):
+        for layer in copies:  # warm every kernel instantiation outside capture
+            for _, q in layer:
+                q(xs[q.in_features])
+        torch.cuda.synchronize()
+        for layer in copies:
+            g = torch.cuda.CUDAGraph()
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(layer) + 1)]
+            with torch.cuda.graph(g, stream=stream):
+                ys = []
+                ev[0].record()
+                for j, (_, q) in enumerate(layer):
+                    ys.append(q(xs[q.in_features]))
+                    ev[j + 1].record()
+            graphs.append(g)
+            events.append(ev)
+            outs.append(ys)
+        torch.cuda.synchronize()
+        for s in range(args.warmup):
+            graphs[s % len(graphs)].replay()
+        torch.cuda.synchronize()
+        # timed region: exactly K steps
+        t0 = time.perf_counter()
+        per_launch = [[] for _ in base]
+        step_ev = []
+        for s in range(args.steps):
+            i = s % len(graphs)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graphs[i].replay()
+            e1.record(stream)
+            step_ev.append((i, e0, e1))
+            if (s + 1) % len(graphs) == 0 or s == args.steps - 1:
+                # read this round's in-graph launch timings before the next replay of the same graph
+                stream.synchronize()
+                for (ii, a, b) in step_ev:
+                    ev = events[ii]
+                    for j in range(len(base)):
+                        per_launch[j].append(ev[j].elapsed_time(ev[j + 1]))
+                step_ev_done = step_ev
+                step_ev = []
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    # decode kernel roofline: bytes of all launches / summed in-graph durations
+    kbytes = [layer_bytes(q, 1) for _, q in base]
+    tot_bytes = sum(kbytes[j] * len(per_launch[j]) for j in range(len(base)))
+    tot_ms = sum(sum(per_launch[j]) for j in range(len(base)))
+    achieved = tot_bytes / (tot_ms * 1e-3) / 1e9
+    detail = {}
+    for j, (name, q) in enumerate(base):
+        avg = sum(per_launch[j]) / len(per_launch[j])
+        detail[name] = {"shape": [q.out_features, q.in_features], "bytes": kbytes[j], "avg_us": round(avg * 1e3, 2),
+                        "GBps": round(kbytes[j] / (avg * 1e-3) / 1e9, 1)}
+    return dict(ms_per_step=ms_per_step, value=value, step_bytes=step_bytes, achieved=achieved, detail=detail,
+                base=base, xs=xs)
+
+
+def bench_prefill(args):
+    import recipes
+    import tensorshrink_amd as ts
+    res = {}
+    M = 2048
+    for bits in (8, 6):
+        opts = dict(bits=bits, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+        lins = []
+        for i, (name, n, k) in enumerate(recipes.LLAMA3_8B_LINEARS[4:]):
+            w = recipes.gaussian_weight(n, k, recipes.layer_seed(4 + i))
+            lins.append((name, ts.QuantLinear(ts.quantize_tensor(w, **opts))))
+            del w
+        xs = {4096: recipes.activations(M, 4096).cuda(), 14336: recipes.activations(M, 14336).cuda()}
+        for _, q in lins:
+            q(xs[q.in_features])
+        torch.cuda.synchronize()
+        times = {name: [] for name, _ in lins}
+        evs = []
+        for s in range(args.prefill_steps):
+            for name, q in lins:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                q(xs[q.in_features])
+                e1.record()
+                evs.append((name, e0, e1))
+        torch.cuda.synchronize()
+        for name, e0, e1 in evs[len(lins):]:  # the first round absorbs the empty-queue start
+            times[name].append(e0.elapsed_time(e1))
+        flops = {name: 2.0 * M * q.out_features * q.in_features for name, q in lins}
+        tot_f = sum(flops[n] * len(times[n]) for n in times)
+        tot_ms = sum(sum(times[n]) for n in times)
+        tflops = tot_f / (tot_ms * 1e-3) / 1e12
+        res[f"{bits}bit"] = {
+            "tflops": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "per_linear_us": {n: round(sum(t) / len(t) * 1e3, 1) for n, t in times.items()}}
+        del lins, xs
+        torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(dec, budget_s: float):
+    """Time the reference CPU fallback forward (oracle restatement) for one
+    layer at M=1, on this host's cores, with the layer's own codes."""
+    import numpy as np
+    from oracle import codec_ref as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    layer = dec["base"]
+    qs = []
+    for name, ql in layer:
+        qt = ql.to_quantized_tensor()
+        q = dict(packed=qt.packed, scale=qt.scale, gmin=qt.gmin, outlier_idx=qt.outlier_idx,
+                 outlier_val=qt.outlier_val, dq_scale_codes=qt.dq_scale_codes, dq_scale_meta=qt.dq_scale_meta,
+                 dq_gmin_codes=qt.dq_gmin_codes, dq_gmin_meta=qt.dq_gmin_meta, codebook=qt.codebook,
+                 _meta=dict(bits=qt.bits, group_size=qt.group_size, rows=qt.rows, cols=qt.cols,
+                            padded_cols=qt.padded_cols, n_groups=qt.n_groups, orig_dtype=qt.orig_dtype))
+        bufs = dict(outlier_row=ql.outlier_row.cpu().numpy(), outlier_col=ql.outlier_col.cpu().numpy(),
+                    outlier_delta=ql.outlier_delta.cpu().numpy())
+        qs.append((q, bufs, dec["xs"][ql.in_features].cpu()))
+    def one():
+        for q, b, x in qs:
+            O.quantlinear_forward_cpu(q, b, x)
+    one()  # warmup
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 10):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(dec["step_bytes"] / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "ms_per_step": round(med * 1e3, 1),
+            "sample": f"{len(times)} CPU forwards of the full M=1 layer (7 linears, bf16 dequant + F.linear, "
+                      f"median); os.cpu_count()={os.cpu_count()}",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--copies", type=int, default=10)
+    ap.add_argument("--prefill-steps", type=int, default=6)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build targets a single MI355X and has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    import tensorshrink_amd  # noqa: F401  (fails loudly without the built library)
+    torch.cuda.set_device(0)
+    opts = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+    log("decode: building layers")
+    dec = bench_decode(args, opts)
+    log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s (kernel {dec['achieved']:.0f} GB/s)")
+    pre = None
+    if not args.no_prefill:
+        log("prefill: M=2048")
+        pre = bench_prefill(args)
+        log(f"prefill: {pre}")
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline(dec, args.cpu_budget)
+        log(f"cpu baseline: {cpu}")
+    out = {
+        "metric": "QuantLinear M=1 HBM GB/s (% peak); M=2048 TFLOPS (% MFMA peak)",
+        "value": round(dec["value"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 activations x 4-bit codes, fp32 accumulate",
+        "data": "synthetic: seeded N(0,0.02) fp16 weights with 0.1% x20 outliers, N(0,1) bf16 activations",
+        "config": {"workload": "decode M=1, Llama-3-8B-shaped layer (q,k,v,o,gate,up,down), 4-bit NF4 + double "
+                               "quant, group 128, outlier_frac 0.001 (BASELINE config 3); 10 rotating copies",
+                   "M": 1, "bytes_per_step": dec["step_bytes"], "frac_of_hbm_peak": round(dec["value"] / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "achieved": round(dec["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "ts::decode_kernel<4,128,bf16> (7 launches per step)", "per_linear": dec["detail"]},
+        "prefill": pre,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -6,6 +6,7 @@ are committed; the arrays are regenerated where they are needed.
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 
@@ -24,13 +25,18 @@ def gaussian_weight(rows: int, cols: int, seed: int, sigma: float = 0.02,
 
 def student_t_weight(rows: int, cols: int, seed: int, df: int = 5, sigma: float = 0.02,
                      dtype: torch.dtype = torch.float16) -> torch.Tensor:
-    """Student-t(df) x sigma weights: z / sqrt(chi2_df / df)."""
+    """Student-t(df) x sigma weights: z / sqrt(chi2_df / df).
+
+    The square root is numpy's (IEEE, correctly rounded): torch's vectorized
+    CPU sqrt is not, and its vector/scalar split depends on the thread count,
+    so it gives different bits on hosts with different core counts."""
     g = torch.Generator().manual_seed(seed)
     z = torch.randn(rows, cols, generator=g)
     c = torch.zeros(rows, cols)
     for _ in range(df):
         c += torch.randn(rows, cols, generator=g) ** 2
-    return (z / torch.sqrt(c / df) * sigma).to(dtype)
+    root = torch.from_numpy(np.sqrt((c / df).numpy()))
+    return (z / root * sigma).to(dtype)
 
 
 def tie_heavy_weight(rows: int, cols: int, seed: int, levels: int = 64,
