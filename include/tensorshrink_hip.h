@@ -69,6 +69,13 @@ typedef struct {
   int64_t stage2_stride;
   const uint16_t* stage2_scale;   /* RVQ only: f16 [rows, n_groups] */
   const uint16_t* stage2_gmin;
+  /* Outliers regrouped per 16-row tile for the decode kernel (derived from the
+   * CSR tables by ts_build_tile_outliers; no counterpart in the reference):
+   * tile t owns slots [t * tile_outlier_cap, (t + 1) * tile_outlier_cap), each
+   * u64 = col | (row - 16 t) << 32 | f16 delta bits << 48; unused slots are 0.
+   * NULL / 0 when the layer has no outliers. */
+  const uint64_t* tile_outliers;
+  int64_t tile_outlier_cap;
 } ts_qlayer;
 
 const char* ts_status_str(int status);
@@ -118,6 +125,18 @@ int ts_dequantize(const ts_qlayer* layer, int mode, const int32_t* outlier_idx, 
  * outlier_row[k] >= r, for r in [0, rows]. */
 int ts_outlier_row_ptr(const int32_t* outlier_row, int64_t n_outliers, int64_t rows, int32_t* row_ptr,
                        void* stream);
+
+/*
+ * Per-tile outlier slots (ts_qlayer.tile_outliers) from the row-sorted CSR
+ * tables. ts_tile_outlier_max writes the largest outlier count of any 16-row
+ * tile to *max_count (device int32); the caller picks cap >= that count and
+ * allocates ceil(rows / 16) * cap slots for ts_build_tile_outliers. Lets the
+ * decode kernel load a tile's outliers at a fixed address instead of through
+ * the row offsets (a dependent load on its critical path).
+ */
+int ts_tile_outlier_max(const int32_t* outlier_row_ptr, int64_t rows, int32_t* max_count, void* stream);
+int ts_build_tile_outliers(const int32_t* outlier_row_ptr, const int32_t* outlier_row, const int32_t* outlier_col,
+                           const uint16_t* outlier_delta, int64_t rows, int64_t cap, uint64_t* slots, void* stream);
 
 /*
  * QuantLinear construction (modules.py:414-448, 649-715): from codec-order

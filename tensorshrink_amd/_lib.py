@@ -38,6 +38,7 @@ class QLayer(ctypes.Structure):
         ("outlier_row", c_vp), ("outlier_col", c_vp), ("outlier_delta", c_vp), ("n_outliers", c_i64),
         ("outlier_row_ptr", c_vp),
         ("stage2_packed", c_vp), ("stage2_stride", c_i64), ("stage2_scale", c_vp), ("stage2_gmin", c_vp),
+        ("tile_outliers", c_vp), ("tile_outlier_cap", c_i64),
     ]
 
 
@@ -65,6 +66,8 @@ PROTOTYPES = {
                                      ctypes.c_int, c_vp]),
     "ts_outlier_row_ptr": (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_vp]),
     "ts_outlier_tables_workspace_bytes": (c_sz, [c_i64, c_i64]),
+    "ts_tile_outlier_max": (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp]),
+    "ts_build_tile_outliers": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "ts_build_outlier_tables": (ctypes.c_int, [ctypes.POINTER(QLayer), c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp,
                                                c_vp, c_sz, c_vp]),
     "ts_topk_workspace_bytes": (c_sz, [c_i64, c_i64]),

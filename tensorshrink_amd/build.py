@@ -19,7 +19,25 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtensorshrink_hip.so")
-SOURCES = ["ts_api.hip", "ts_decode.hip", "ts_prefill.hip", "ts_aux.hip", "ts_quantize.hip"]
+SOURCES = [
+    "ts_api.hip",
+    "ts_decode.hip",
+    "ts_decode_b2_g64.hip",
+    "ts_decode_b2_g128.hip",
+    "ts_decode_b2_g256.hip",
+    "ts_decode_b4_g32.hip",
+    "ts_decode_b4_g64.hip",
+    "ts_decode_b4_g128.hip",
+    "ts_decode_b4_g256.hip",
+    "ts_decode_b6_g64.hip",
+    "ts_decode_b6_g128.hip",
+    "ts_decode_b8_g32.hip",
+    "ts_decode_b8_g64.hip",
+    "ts_decode_b8_g128.hip",
+    "ts_prefill.hip",
+    "ts_aux.hip",
+    "ts_quantize.hip",
+]
 ARCH = os.environ.get("TS_OFFLOAD_ARCH", "gfx950")
 
 

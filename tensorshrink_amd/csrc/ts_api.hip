@@ -13,6 +13,9 @@ int generic_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ld
 int dequantize(const ts_qlayer* L, int mode, const int32_t* oidx, const uint16_t* oval, int64_t n_oidx,
                void* w_out, int64_t ldw, int dt, hipStream_t st);
 int outlier_row_ptr(const int32_t* row, int64_t n, int64_t rows, int32_t* row_ptr, hipStream_t st);
+int tile_outlier_max(const int32_t* rp, int64_t rows, int32_t* out, hipStream_t st);
+int build_tile_outliers(const int32_t* rp, const int32_t* orow, const int32_t* ocol, const uint16_t* odelta,
+                        int64_t rows, int64_t cap, uint64_t* slots, hipStream_t st);
 size_t outlier_tables_ws(int64_t n);
 int build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n, int32_t* orow,
                          int32_t* ocol, uint16_t* odelta, int32_t* row_ptr, void* ws, size_t ws_bytes,
@@ -51,6 +54,7 @@ static bool layer_ok(const ts_qlayer* L) {
   if (L->n_outliers > 0 && (!L->outlier_row || !L->outlier_col || !L->outlier_delta || !L->outlier_row_ptr))
     return false;
   if (L->bits == 6 && (!L->stage2_packed || !L->stage2_scale || !L->stage2_gmin)) return false;
+  if (L->tile_outliers && L->tile_outlier_cap <= 0) return false;
   return true;
 }
 
@@ -123,6 +127,17 @@ int ts_outlier_row_ptr(const int32_t* outlier_row, int64_t n, int64_t rows, int3
 size_t ts_outlier_tables_workspace_bytes(int64_t n, int64_t rows) {
   (void)rows;
   return n > 0 ? ts::outlier_tables_ws(n) : 0;
+}
+
+int ts_tile_outlier_max(const int32_t* row_ptr, int64_t rows, int32_t* max_count, void* stream) {
+  if (!row_ptr || !max_count || rows <= 0) return TS_BAD_ARG;
+  return ts::tile_outlier_max(row_ptr, rows, max_count, S(stream));
+}
+
+int ts_build_tile_outliers(const int32_t* row_ptr, const int32_t* orow, const int32_t* ocol, const uint16_t* odelta,
+                           int64_t rows, int64_t cap, uint64_t* slots, void* stream) {
+  if (!row_ptr || !orow || !ocol || !odelta || !slots || rows <= 0 || cap <= 0) return TS_BAD_ARG;
+  return ts::build_tile_outliers(row_ptr, orow, ocol, odelta, rows, cap, slots, S(stream));
 }
 
 int ts_build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n, int32_t* orow,

@@ -218,6 +218,56 @@ int build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t*
   return TS_OK;
 }
 
+// Largest outlier count over 16-row tiles: one workgroup, strided over tiles.
+__global__ __launch_bounds__(1024) void tile_max_kernel(const int32_t* __restrict__ rp, int64_t rows,
+                                                        int32_t* __restrict__ out) {
+  __shared__ int32_t part[1024];
+  const int64_t n_tiles = ts_cdiv(rows, 16);
+  int32_t best = 0;
+  for (int64_t t = threadIdx.x; t < n_tiles; t += 1024) {
+    const int32_t c = rp[std::min<int64_t>(16 * t + 16, rows)] - rp[16 * t];
+    best = c > best ? c : best;
+  }
+  part[threadIdx.x] = best;
+  __syncthreads();
+  for (int s = 512; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s && part[threadIdx.x + s] > part[threadIdx.x]) part[threadIdx.x] = part[threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = part[0];
+}
+
+// Slot i of tile t: outlier rp[16t] + i of the row-sorted tables, or 0.
+__global__ __launch_bounds__(256) void tile_slots_kernel(const int32_t* __restrict__ rp, const int32_t* __restrict__ orow,
+                                                         const int32_t* __restrict__ ocol,
+                                                         const uint16_t* __restrict__ odelta, int64_t rows,
+                                                         int64_t cap, uint64_t* __restrict__ slots) {
+  const int64_t t = blockIdx.x;
+  const int32_t k0 = rp[16 * t], k1 = rp[std::min<int64_t>(16 * t + 16, rows)];
+  for (int64_t i = threadIdx.x; i < cap; i += 256) {
+    const int64_t k = k0 + i;
+    uint64_t v = 0;
+    if (k < k1)
+      v = (uint64_t)(uint32_t)ocol[k] | ((uint64_t)(uint32_t)(orow[k] - 16 * t) << 32) |
+          ((uint64_t)odelta[k] << 48);
+    slots[t * cap + i] = v;
+  }
+}
+
+int tile_outlier_max(const int32_t* rp, int64_t rows, int32_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(tile_max_kernel, dim3(1), dim3(1024), 0, st, rp, rows, out);
+  TS_CHECK_LAUNCH();
+  return TS_OK;
+}
+
+int build_tile_outliers(const int32_t* rp, const int32_t* orow, const int32_t* ocol, const uint16_t* odelta,
+                        int64_t rows, int64_t cap, uint64_t* slots, hipStream_t st) {
+  hipLaunchKernelGGL(tile_slots_kernel, dim3((unsigned)ts_cdiv(rows, 16)), dim3(256), 0, st, rp, orow, ocol, odelta,
+                     rows, cap, slots);
+  TS_CHECK_LAUNCH();
+  return TS_OK;
+}
+
 int apply_outlier_correction(float* out, int64_t M, int64_t ldo, const void* x, int64_t ldx, int xdt,
                              const int32_t* row_ptr, const int32_t* col, const uint16_t* delta, int64_t rows,
                              hipStream_t st) {

@@ -70,6 +70,34 @@ TS_DEV ts_u32x4 ts_ld16(const void* p) { return *reinterpret_cast<const ts_u32x4
 TS_DEV ts_u32x2 ts_ld8(const void* p) { return *reinterpret_cast<const ts_u32x2*>(p); }
 TS_DEV uint32_t ts_ld4(const void* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
+// Kernel-argument pinning. The compiler treats kernel arguments as invariant
+// loads and re-fetches them lazily, in dependent batches of scalar loads (each
+// a memory round trip) wherever SGPR pressure is high. Passing a value
+// through an empty asm makes it opaque, so it is fetched once, up front, and
+// kept in SGPRs. Pointers are pinned in the global address space so that
+// accesses through them stay global (not flat) instructions.
+template <typename T>
+TS_DEV void ts_pin_scalar(T& v) {
+  asm volatile("" : "+s"(v));
+}
+template <typename T>
+TS_DEV void ts_pin_global(T*& p) {
+  auto g = (__attribute__((address_space(1))) T*)p;
+  asm volatile("" : "+s"(g));
+  p = (T*)g;
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS ops
+// (lgkmcnt(0)) but not for its in-flight global loads, unlike __syncthreads,
+// whose workgroup fence drains vmcnt. The empty asm statements keep the
+// compiler from moving memory accesses across it.
+TS_DEV void ts_lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt=63, expcnt=7, lgkmcnt=0
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Host-side helpers shared by the entry points.
 #define TS_CHECK_LAUNCH()                                   \
   do {                                                      \

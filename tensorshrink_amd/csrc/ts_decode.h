@@ -1,0 +1,645 @@
+// Decode (M <= 16) quantized linear: y[M, N] = x[M, K] W^T + outliers + bias.
+//
+// Replaces the reference's fused Triton GEMV/skinny-GEMM
+// (triton_kernels.py:278-541, dispatched at modules.py:881-894) and its
+// standalone outlier pass (triton_kernels.py:543-576, 940-941).
+//
+// Work unit: a tile of 16 weight rows x all of K. A workgroup of 4 waves owns
+// a tile (persistent over tiles only when more tiles than resident workgroups);
+// wave w owns a contiguous run of the tile's group batches.
+//   * MFMA f32_16x16x32 (bf16 or f16): lane l owns W row r0 + l%16 (B column)
+//     and x row l%16 (A row); lane group q = l/16 owns a quarter of each group,
+//     so one group is GS/32 MFMAs over that lane set.
+//   * Each lane streams its quarter-group of packed codes with 8/16-byte loads,
+//     U groups per batch, double-buffered in registers across batches and
+//     tiles. A batch's per-group metadata comes in a few vector loads: U
+//     scale/double-quant codes in one load when the batch is aligned, and the
+//     (at most two) double-quant super-groups it spans in four.
+//   * Codes become bf16/f16 pairs through an LDS table indexed by the packed
+//     byte (4-bit: one u32 = two codes; 2-bit: one u64 = four codes), kept in
+//     REP bank-private copies so random bytes never collide on a bank.
+//   * The per-group affine is factorised out of the MFMA:
+//         y += s[n,g] * (x . cb[c]) + gmin[n,g] * (x . 1)
+//     with both dot products on the matrix core and s/gmin in float32
+//     (rebuilt from double-quant codes in-register, modules.py:573-579).
+//   * x is staged once per workgroup in LDS when M*K fits, else read per group.
+//   * Per tile: the waves' partials reduced in LDS, the tile's row-sorted
+//     outliers (CSR slice, loaded one tile ahead) added with LDS float atomics,
+//     then bias and the compute-dtype store.
+//
+// Latency rules the code follows (each was measured to matter on gfx950):
+//   * every load of a phase is issued before anything waits: loads are
+//     unconditional (addresses clamped into valid memory, predicates applied
+//     where the value is used), since a load under a branch is followed by a
+//     wait at the join;
+//   * kernel arguments are pinned in SGPRs at entry (one batch of scalar loads
+//     instead of several dependent ones);
+//   * LDS barriers wait for LDS traffic only (ts_lds_barrier), never for the
+//     weight loads in flight.
+#pragma once
+#include <algorithm>
+
+#include "ts_common.h"
+
+namespace ts {
+
+struct DecodeArgs {
+  const uint8_t* packed;
+  int64_t pstride;
+  const uint16_t* scale;
+  const uint16_t* gmin;
+  const uint8_t* dqsc;
+  const uint16_t* dqsm;
+  const uint8_t* dqgc;
+  const uint16_t* dqgm;
+  uint32_t dq_gs;
+  const uint8_t* s2packed;
+  int64_t s2stride;
+  const uint16_t* s2scale;
+  const uint16_t* s2gmin;
+  const uint64_t* slots;     // per-tile outlier slots (ts_qlayer.tile_outliers), or any valid
+                             // 8-byte array when cap == 0
+  int32_t cap;               // slots per tile (0: no outliers)
+  const uint16_t* x;
+  int64_t ldx;
+  void* y;
+  int64_t ldy;
+  int y_dtype;
+  const uint16_t* bias;      // nullptr when there is no bias
+  int64_t N;
+  int64_t cols;
+  int64_t K;                 // padded columns
+  int64_t n_groups;
+  int64_t n_tiles;
+  int M;
+  const float* cbsrc;        // codebook, or any valid float array when cb_is_table == 0
+  int cb_is_table;
+  const uint16_t* bias_src;  // bias, or any valid array when there is none
+  int64_t bias_mul;          // 1 with a bias, else 0
+};
+
+constexpr size_t DEC_XLDS_MAX = 32 * 1024;  // activations staged in LDS up to this size
+
+template <bool BF16>
+TS_DEV uint32_t pack2(float lo, float hi) {
+  return (uint32_t)XT<BF16>::from_f(lo) | ((uint32_t)XT<BF16>::from_f(hi) << 16);
+}
+
+template <int NB>
+struct Bytes {
+  uint32_t d[(NB + 3) / 4];
+};
+
+// NB bytes (1, 2, 4, 8, 16 or 32) from an NB-aligned address, one or two loads.
+template <int NB>
+TS_DEV Bytes<NB> load_bytes(const uint8_t* p) {
+  Bytes<NB> b;
+  if constexpr (NB == 32) {
+    ts_u32x4 v0 = ts_ld16(p), v1 = ts_ld16(p + 16);
+    b.d[0] = v0.x; b.d[1] = v0.y; b.d[2] = v0.z; b.d[3] = v0.w;
+    b.d[4] = v1.x; b.d[5] = v1.y; b.d[6] = v1.z; b.d[7] = v1.w;
+  } else if constexpr (NB == 16) {
+    ts_u32x4 v = ts_ld16(p);
+    b.d[0] = v.x; b.d[1] = v.y; b.d[2] = v.z; b.d[3] = v.w;
+  } else if constexpr (NB == 8) {
+    ts_u32x2 v = ts_ld8(p);
+    b.d[0] = v.x; b.d[1] = v.y;
+  } else if constexpr (NB == 4) {
+    b.d[0] = ts_ld4(p);
+  } else if constexpr (NB == 2) {
+    b.d[0] = *reinterpret_cast<const uint16_t*>(p);
+  } else {
+    static_assert(NB == 1, "unsupported chunk");
+    b.d[0] = *p;
+  }
+  return b;
+}
+
+TS_DEV uint32_t byte_of(const uint32_t* d, int i) { return (d[i >> 2] >> (8 * (i & 3))) & 0xffu; }
+TS_DEV uint32_t half_of(const uint32_t* d, int i) { return (d[i >> 1] >> (16 * (i & 1))) & 0xffffu; }
+
+template <int BITS, int GS, bool RVQ>
+struct DecGeom {
+  static constexpr int GB = GS * BITS / 8;  // packed bytes per row per group
+  static constexpr int LB = GB / 4;         // bytes per lane per group
+  static constexpr int GB2 = GS / 4;        // RVQ stage-2 bytes per row per group
+  static constexpr int LB2 = GB2 / 4;
+  static constexpr int U0 = (LB + (RVQ ? LB2 : 0)) > 0 ? 64 / (LB + (RVQ ? LB2 : 0)) : 8;
+  // groups per batch (~64 B of codes per lane), a power of two in [1, 8]
+  static constexpr int U = U0 >= 8 ? 8 : (U0 >= 4 ? 4 : (U0 >= 2 ? 2 : 1));
+};
+
+// W: waves per workgroup (4, 8 or 16), all on the same tile, each owning a
+// contiguous run of its group batches. Without LOOP every wave has at most
+// two batches and the kernel is straight-line code: the host picks the
+// smallest W for which that holds. LOOP streams longer runs through the two
+// register buffers.
+// AL: the row's group count is a multiple of U, so every batch starts on a
+// multiple of U in the row-major (row, group) metadata arrays and its U codes
+// / scales come in one aligned vector load.
+// Occupancy: at most 128 VGPRs (4 waves per SIMD, 16 per CU), so 1024 waves
+// of 16-row tiles are resident at once across 256 CUs.
+template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, bool XLDS, bool DQ, bool AL, int W, bool LOOP>
+__global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in) {
+  constexpr int NT = 64 * W;
+  extern __shared__ __align__(16) unsigned char smem[];
+  using Geo = DecGeom<BITS, GS, RVQ>;
+  constexpr int GB = Geo::GB, LB = Geo::LB, GB2 = Geo::GB2, LB2 = Geo::LB2, U = Geo::U;
+  constexpr int NMF = (BITS == 8 && CB8) ? GS / 16 : GS / 32;  // MFMAs per group
+  constexpr int CPM = (BITS == 8 && CB8) ? 4 : 8;              // codes per lane per MFMA
+  constexpr bool USE_T4 = (BITS == 4);
+  constexpr bool USE_T2 = (BITS == 2) || RVQ;
+  constexpr bool USE_T8 = (BITS == 8) && CB8;
+  constexpr int NW8 = (U + 3) / 4;   // words holding U bytes
+  constexpr int NW16 = (U + 1) / 2;  // words holding U halves
+  constexpr int NSC = AL ? (DQ ? NW8 : NW16) : U;
+
+  // Every kernel argument is fetched here, in one batch of scalar loads, and
+  // made opaque so the compiler keeps it in SGPRs. Otherwise it re-fetches
+  // arguments lazily (they are invariant loads) in several dependent
+  // batches, each a memory round trip on every workgroup's critical path.
+  DecodeArgs a = a_in;
+#define TS_PG(f) ts_pin_global(a.f)
+#define TS_PS(f) ts_pin_scalar(a.f)
+  TS_PG(packed); TS_PG(scale); TS_PG(gmin); TS_PG(dqsc); TS_PG(dqsm); TS_PG(dqgc); TS_PG(dqgm); TS_PG(x); TS_PG(y);
+  TS_PG(slots); TS_PG(cbsrc); TS_PG(bias_src);
+  TS_PS(pstride); TS_PS(dq_gs); TS_PS(ldx); TS_PS(ldy); TS_PS(N); TS_PS(cols); TS_PS(K); TS_PS(n_groups);
+  TS_PS(n_tiles); TS_PS(M); TS_PS(cb_is_table); TS_PS(cap); TS_PS(bias_mul); TS_PS(y_dtype);
+  if constexpr (RVQ) { TS_PG(s2packed); TS_PS(s2stride); TS_PG(s2scale); TS_PG(s2gmin); }
+#undef TS_PG
+#undef TS_PS
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n = lane & 15;
+  const int q = lane >> 4;
+  const int rsl = lane & (REP - 1);
+
+  // ---- LDS carve-up ------------------------------------------------------
+  unsigned char* sp = smem;
+  uint32_t* t4 = nullptr;
+  uint2* t2 = nullptr;
+  uint32_t* t8 = nullptr;
+  if constexpr (USE_T4) { t4 = reinterpret_cast<uint32_t*>(sp); sp += 256 * REP * 4; }
+  if constexpr (USE_T2) { t2 = reinterpret_cast<uint2*>(sp); sp += 256 * REP * 8; }
+  if constexpr (USE_T8) { t8 = reinterpret_cast<uint32_t*>(sp); sp += 256 * REP * 4; }
+  float* red = reinterpret_cast<float*>(sp);       // [W][64][4]
+  sp += W * 64 * 4 * 4;
+  float* ys = reinterpret_cast<float*>(sp);        // [16][17]
+  sp += 16 * 17 * 4;
+  float* cbs = reinterpret_cast<float*>(sp);       // [256] staged codebook
+  sp += 256 * 4;
+  uint32_t* xzero = reinterpret_cast<uint32_t*>(sp);  // 16 zero bytes: x rows >= M read here
+  sp += 16;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(sp);  // [M][K] staged activations (XLDS)
+
+  // ---- per-wave share of every tile ----------------------------------------
+  // The row's T batches of U groups are split into contiguous runs, one per
+  // wave; every wave steps nb batches (a short run's extra batch is dead).
+  // (32-bit index math: groups per row and tile counts are far below 2^31.)
+  const int G = (int)a.n_groups;
+  const int T = (G + U - 1) / U;
+  const int g_lo = U * ((T * wave) / W);
+  const int g_hi = min(G, U * ((T * (wave + 1)) / W));
+  const int nb = (T + W - 1) / W;
+  const bool xrow = n < a.M;
+  constexpr uint32_t ONE = XT<BF16>::ONE;
+  const ts_u32x4 ones = CB8 ? ts_u32x4{ONE, ONE, ONE, ONE}
+                            : ts_u32x4{ONE | (ONE << 16), ONE | (ONE << 16), ONE | (ONE << 16), ONE | (ONE << 16)};
+
+  // Raw loads only: nothing here consumes loaded data, so issuing a batch
+  // never waits on memory.
+  struct Batch {
+    Bytes<LB> w[U];
+    Bytes<(LB2 > 0 ? LB2 : 1)> w2[U];
+    uint32_t sc[NSC], gc[NSC];      // DQ codes (bytes), or f16 scale / gmin bits
+    uint32_t smA, smB, gmA, gmB;    // DQ (meta_scale, meta_min) f16 pairs of the two super-groups
+    int split;                      // groups u < split use the first super-group
+    uint32_t s2s[RVQ ? (AL ? NW16 : U) : 1], s2g[RVQ ? (AL ? NW16 : U) : 1];  // RVQ stage-2 f16 bits
+    uint32_t live;                  // bit u set when group u of the batch exists
+  };
+
+  auto load_batch = [&](int64_t tile, int b, Batch& B) {
+    const int gb = g_lo + b * U;
+    const bool any = gb < g_hi;
+    // a dead batch (past the wave's run) reads the tile's first row at one
+    // address per load: one cache line, never used
+    const int64_t r = any ? min(tile * 16 + n, a.N - 1) : min(tile * 16, a.N - 1);
+    const uint8_t* wp = a.packed + r * a.pstride + (any ? q * LB : 0);
+    const int gb0 = any ? gb : g_lo;  // a dead batch re-reads the wave's first groups
+    int gg[U];
+    B.live = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = gb + u < g_hi;
+      B.live |= live ? (1u << u) : 0u;
+      gg[u] = live ? gb + u : gb0;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) B.w[u] = load_bytes<LB>(wp + (int64_t)gg[u] * GB);
+    const int64_t rowg = r * G;
+    if constexpr (RVQ) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        B.w2[u] = load_bytes<LB2>(a.s2packed + r * a.s2stride + q * LB2 + (int64_t)gg[u] * GB2);
+      if constexpr (AL) {
+        const Bytes<2 * U> vs = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.s2scale + rowg + gb0));
+        const Bytes<2 * U> vg = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.s2gmin + rowg + gb0));
+#pragma unroll
+        for (int i = 0; i < NW16; ++i) { B.s2s[i] = vs.d[i]; B.s2g[i] = vg.d[i]; }
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) { B.s2s[u] = a.s2scale[rowg + gg[u]]; B.s2g[u] = a.s2gmin[rowg + gg[u]]; }
+      }
+    }
+    if constexpr (DQ) {
+      if constexpr (AL) {
+        const Bytes<U> vs = load_bytes<U>(a.dqsc + rowg + gb0);
+        const Bytes<U> vg = load_bytes<U>(a.dqgc + rowg + gb0);
+#pragma unroll
+        for (int i = 0; i < NW8; ++i) { B.sc[i] = vs.d[i]; B.gc[i] = vg.d[i]; }
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) { B.sc[u] = a.dqsc[rowg + gg[u]]; B.gc[u] = a.dqgc[rowg + gg[u]]; }
+      }
+      // The batch's live groups are consecutive, so they span at most two
+      // super-groups (dq_gs >= U is checked on the host).
+      const int nlive = max(1, min(U, g_hi - gb));
+      const uint32_t f0 = (uint32_t)(rowg + gb0);
+      const uint32_t sup0 = f0 / a.dq_gs;
+      const uint32_t sup1 = (f0 + (uint32_t)(any ? nlive - 1 : 0)) / a.dq_gs;
+      B.split = (int)min((uint32_t)U, (sup0 + 1) * a.dq_gs - f0);
+      B.smA = *reinterpret_cast<const uint32_t*>(a.dqsm + 2 * sup0);
+      B.smB = *reinterpret_cast<const uint32_t*>(a.dqsm + 2 * sup1);
+      B.gmA = *reinterpret_cast<const uint32_t*>(a.dqgm + 2 * sup0);
+      B.gmB = *reinterpret_cast<const uint32_t*>(a.dqgm + 2 * sup1);
+    } else {
+      if constexpr (AL) {
+        const Bytes<2 * U> vs = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.scale + rowg + gb0));
+        const Bytes<2 * U> vg = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.gmin + rowg + gb0));
+#pragma unroll
+        for (int i = 0; i < NW16; ++i) { B.sc[i] = vs.d[i]; B.gc[i] = vg.d[i]; }
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) { B.sc[u] = a.scale[rowg + gg[u]]; B.gc[u] = a.gmin[rowg + gg[u]]; }
+      }
+      B.smA = B.smB = B.gmA = B.gmB = 0u;
+      B.split = U;
+    }
+  };
+
+  auto compute_batch = [&](int b, const Batch& B, ts_f32x4& yacc) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int g = g_lo + b * U + u;
+      if (!((B.live >> u) & 1u)) break;  // wave-uniform
+      float s_, gm_;
+      if constexpr (DQ) {  // modules.py:573-579: code * meta_scale + meta_min in float32
+        const float cs = (float)(AL ? byte_of(B.sc, u) : B.sc[u]);
+        const float cg = (float)(AL ? byte_of(B.gc, u) : B.gc[u]);
+        const uint32_t ms = u < B.split ? B.smA : B.smB;
+        const uint32_t mg = u < B.split ? B.gmA : B.gmB;
+        s_ = __fadd_rn(__fmul_rn(cs, ts_h2f(ms & 0xffffu)), ts_h2f(ms >> 16));
+        gm_ = __fadd_rn(__fmul_rn(cg, ts_h2f(mg & 0xffffu)), ts_h2f(mg >> 16));
+      } else {
+        s_ = ts_h2f((uint16_t)(AL ? half_of(B.sc, u) : B.sc[u]));
+        gm_ = ts_h2f((uint16_t)(AL ? half_of(B.gc, u) : B.gc[u]));
+      }
+      // Phase 1: every LDS read of the group (x operands and code-table
+      // entries) is issued before the first MFMA, so the reads overlap
+      // instead of each MFMA waiting out one LDS round trip.
+      const int c0 = g * GS + q * (GS / 4);
+      ts_u32x4 xa[NMF], bv[NMF], bv2[RVQ ? NMF : 1];
+#pragma unroll
+      for (int j = 0; j < NMF; ++j) {
+        const int col = c0 + j * CPM;
+        if constexpr (CPM == 8) {
+          if constexpr (XLDS) {
+            const void* xp = xrow ? static_cast<const void*>(xs + n * a.K + col) : static_cast<const void*>(xzero);
+            xa[j] = *reinterpret_cast<const ts_u32x4*>(xp);
+          } else {
+            const ts_u32x4 v = ts_ld16(a.x + min(n, a.M - 1) * a.ldx + min(col, (int)a.cols - 8));
+            xa[j] = (xrow && col < a.cols) ? v : ts_u32x4{0u, 0u, 0u, 0u};
+          }
+        } else {
+          ts_u32x2 v;
+          if constexpr (XLDS) {
+            const void* xp = xrow ? static_cast<const void*>(xs + n * a.K + col) : static_cast<const void*>(xzero);
+            v = *reinterpret_cast<const ts_u32x2*>(xp);
+          } else {
+            const ts_u32x2 l = ts_ld8(a.x + min(n, a.M - 1) * a.ldx + min(col, (int)a.cols - 4));
+            v = (xrow && col < a.cols) ? l : ts_u32x2{0u, 0u};
+          }
+          // (x_k, x_k) pairs so one (hi, lo) table word multiplies x_k twice.
+          xa[j] = ts_u32x4{__builtin_amdgcn_perm(v.x, v.x, 0x05040100u), __builtin_amdgcn_perm(v.x, v.x, 0x07060302u),
+                           __builtin_amdgcn_perm(v.y, v.y, 0x05040100u), __builtin_amdgcn_perm(v.y, v.y, 0x07060302u)};
+        }
+        if constexpr (BITS == 4) {
+          const int b0 = 4 * j;
+          bv[j] = ts_u32x4{t4[byte_of(B.w[u].d, b0 + 0) * REP + rsl], t4[byte_of(B.w[u].d, b0 + 1) * REP + rsl],
+                           t4[byte_of(B.w[u].d, b0 + 2) * REP + rsl], t4[byte_of(B.w[u].d, b0 + 3) * REP + rsl]};
+        } else if constexpr (BITS == 2) {
+          const uint2 e0 = t2[byte_of(B.w[u].d, 2 * j + 0) * REP + rsl];
+          const uint2 e1 = t2[byte_of(B.w[u].d, 2 * j + 1) * REP + rsl];
+          bv[j] = ts_u32x4{e0.x, e0.y, e1.x, e1.y};
+        } else if constexpr (CB8) {
+          bv[j] = ts_u32x4{t8[byte_of(B.w[u].d, 4 * j + 0) * REP + rsl], t8[byte_of(B.w[u].d, 4 * j + 1) * REP + rsl],
+                           t8[byte_of(B.w[u].d, 4 * j + 2) * REP + rsl], t8[byte_of(B.w[u].d, 4 * j + 3) * REP + rsl]};
+        } else {
+          uint32_t pr[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float f0 = (float)byte_of(B.w[u].d, 8 * j + 2 * t);
+            const float f1 = (float)byte_of(B.w[u].d, 8 * j + 2 * t + 1);
+            if constexpr (BF16)
+              pr[t] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0),
+                                            0x07060302u);
+            else
+              pr[t] = pack2<false>(f0, f1);
+          }
+          bv[j] = ts_u32x4{pr[0], pr[1], pr[2], pr[3]};
+        }
+        if constexpr (RVQ) {
+          const uint2 e0 = t2[byte_of(B.w2[u].d, 2 * j + 0) * REP + rsl];
+          const uint2 e1 = t2[byte_of(B.w2[u].d, 2 * j + 1) * REP + rsl];
+          bv2[j] = ts_u32x4{e0.x, e0.y, e1.x, e1.y};
+        }
+      }
+      // Phase 2: the group's MFMAs.
+      ts_f32x4 aw = {0.f, 0.f, 0.f, 0.f};
+      ts_f32x4 ax = {0.f, 0.f, 0.f, 0.f};
+      ts_f32x4 aw2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NMF; ++j) {
+        aw = ts_mfma16x16x32<BF16>(xa[j], bv[j], aw);
+        ax = ts_mfma16x16x32<BF16>(xa[j], ones, ax);
+        if constexpr (RVQ) aw2 = ts_mfma16x16x32<BF16>(xa[j], bv2[j], aw2);
+      }
+      float s2_ = 0.f, g2_ = 0.f;
+      if constexpr (RVQ) {
+        s2_ = ts_h2f((uint16_t)(AL ? half_of(B.s2s, u) : B.s2s[u]));
+        g2_ = ts_h2f((uint16_t)(AL ? half_of(B.s2g, u) : B.s2g[u]));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = yacc[i];
+        v = __builtin_fmaf(s_, aw[i], v);
+        v = __builtin_fmaf(gm_, ax[i], v);
+        if constexpr (RVQ) {
+          v = __builtin_fmaf(s2_, aw2[i], v);
+          v = __builtin_fmaf(g2_, ax[i], v);
+        }
+        yacc[i] = v;
+      }
+    }
+  };
+
+  // ---- one tile per workgroup, batches double-buffered ----------------------
+  const int64_t tile = blockIdx.x;
+  if (tile >= a.n_tiles) return;
+  const int64_t r0 = tile * 16;
+  ts_f32x4 yacc = {0.f, 0.f, 0.f, 0.f};
+
+  // Every load of the tile is issued up front, none depending on another: x
+  // chunks, the codebook, both weight batches, the tile's outlier slots and
+  // the bias.
+  // x -> LDS ([M][K] bf16/f16) with direct global->LDS loads: each wave
+  // instruction moves one 1 KB chunk (16 B per lane, lane-contiguous), so no
+  // registers are held while the weight loads are issued. Lanes past the
+  // end of x read a clamped (valid) address; their bytes land in the padded
+  // tail of the buffer or in the column padding, which is zeroed below.
+  // (32-bit arithmetic: with x staged, M * K * 2 <= DEC_XLDS_MAX.)
+  const uint32_t kK = (uint32_t)a.K;
+  const uint32_t xchunks = XLDS ? ((uint32_t)a.M * kK * 2u + 1023u) / 1024u : 0u;
+  // (unrolled to a compile-time bound with uniform predicates: a loop with a
+  // runtime trip count would hide from the compiler how many loads follow
+  // each one, and every later wait would become a full drain)
+  constexpr int XCW = XLDS ? (int)((DEC_XLDS_MAX / 1024 + W - 1) / W) : 0;  // max chunks per wave
+  if constexpr (XLDS) {
+#pragma unroll
+    for (int i = 0; i < XCW; ++i) {
+      const uint32_t c = (uint32_t)(wave + i * W);
+      if (c < xchunks) {
+        const uint32_t e = c * 512u + (uint32_t)lane * 8u;
+        const uint32_t m = min(e / kK, (uint32_t)a.M - 1u);
+        const uint32_t k = min(e - (e / kK) * kK, (uint32_t)a.cols - 8u);
+        __builtin_amdgcn_global_load_lds(a.x + (int64_t)m * a.ldx + k,
+                                         (__attribute__((address_space(3))) void*)(xs + c * 512u), 16, 0, 0);
+      }
+    }
+  }
+  constexpr int NCB = 1 << (RVQ ? 4 : BITS);
+  const int cbi = tid & 255;  // staged codebook slot (every writer of a slot writes the same value)
+  const float cbraw = a.cbsrc[(cbi < NCB && a.cb_is_table) ? cbi : 0];
+  Batch bufA, bufB;
+  load_batch(tile, 0, bufA);
+  load_batch(tile, 1, bufB);  // (a dead batch when nb == 1)
+  // This tile's outlier slots sit at a fixed address (no dependent load):
+  // each thread takes slots tid and tid + NT; more (rare) are read in the
+  // epilogue. Indices past cap read a valid slot whose value is dropped.
+  const int64_t sbase = tile * a.cap;
+  const int capm1 = max(a.cap - 1, 0);
+  const uint64_t slot0 = a.slots[sbase + min(tid, capm1)];
+  const uint64_t slot1 = a.slots[sbase + min(tid + NT, capm1)];
+  // bias of the output this thread stores (16 rows x M; entry 0 of a valid
+  // array when there is no bias)
+  const uint16_t bias_v = a.bias_src[min(r0 + (tid & 15), a.N - 1) * a.bias_mul];
+
+  // unconditional store (threads tid, tid + 256, ... write the same value to
+  // slot tid % 256): a store under `tid < NCB` would let the compiler sink
+  // the codebook load next to it and wait there for every load issued before.
+  cbs[cbi] = a.cb_is_table ? cbraw : (float)cbi;
+  if (tid < 4) xzero[tid] = 0u;
+  if constexpr (XLDS) {
+    // Each wave waits for its own chunks before the barrier (reading one word
+    // of the last one back makes the compiler emit the wait). The compiler's
+    // wait-count model treats direct-to-LDS loads as completing out of order
+    // with ordinary loads, so this wait also covers the weight loads issued
+    // after them; compute needs those next anyway, and no load in this kernel
+    // depends on another, so nothing else is serialised behind it.
+    uint32_t last = 0;
+    if ((uint32_t)wave < xchunks) {
+      const uint32_t c_last = (uint32_t)wave + ((xchunks - 1u - (uint32_t)wave) / W) * W;
+      last = reinterpret_cast<const uint32_t*>(xs)[c_last * 256u + (uint32_t)lane];
+    }
+    asm volatile("" ::"v"(last));
+    if (kK > (uint32_t)a.cols) {  // column padding: x is zero there
+      __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): all of this wave's chunks landed
+      const uint32_t padw = kK - (uint32_t)a.cols;
+      for (uint32_t e = tid; e < (uint32_t)a.M * padw; e += NT) {
+        const uint32_t m = e / padw;
+        xs[m * kK + (uint32_t)a.cols + (e - m * padw)] = 0;
+      }
+    }
+  }
+  ts_lds_barrier();
+  for (int e = tid; e < 256 * REP; e += NT) {
+    const int b = e / REP;
+    if constexpr (USE_T4) t4[e] = pack2<BF16>(cbs[b & 15], cbs[b >> 4]);
+    if constexpr (USE_T2) {
+      // RVQ stage 2 is always a uniform grid; a 2-bit layer uses its codebook.
+      float v[4];
+      for (int j = 0; j < 4; ++j) {
+        const int c = (b >> (2 * j)) & 3;
+        v[j] = RVQ ? (float)c : cbs[c];
+      }
+      t2[e] = make_uint2(pack2<BF16>(v[0], v[1]), pack2<BF16>(v[2], v[3]));
+    }
+    if constexpr (USE_T8) {
+      const float v = cbs[b];
+      const uint16_t hb = XT<BF16>::from_f(v);
+      const uint16_t lb = XT<BF16>::from_f(v - XT<BF16>::to_f(hb));
+      t8[e] = (uint32_t)hb | ((uint32_t)lb << 16);
+    }
+  }
+  ts_lds_barrier();
+
+  // Two register buffers, bound statically (a runtime-indexed pair would live
+  // in scratch memory). Without LOOP both were issued in the prologue (the
+  // second is dead when nb == 1) and the compiler waits for exactly the one
+  // being consumed. With LOOP each is refilled right after its batch is
+  // consumed, unconditionally (a batch past the end reads one uniform cache
+  // line and is never used), so every path into a compute step has issued
+  // the same loads in the same order.
+  if constexpr (!LOOP) {
+    compute_batch(0, bufA, yacc);
+    if (nb > 1) compute_batch(1, bufB, yacc);
+  } else {
+    for (int b = 0; b < nb; b += 2) {
+      compute_batch(b, bufA, yacc);
+      load_batch(tile, b + 2, bufA);
+      if (b + 1 >= nb) break;
+      compute_batch(b + 1, bufB, yacc);
+      load_batch(tile, b + 3, bufB);
+    }
+  }
+
+  // ---- epilogue: reduce the waves' partials, outliers, bias, store ----------
+  *reinterpret_cast<ts_f32x4*>(red + (wave * 64 + lane) * 4) = yacc;
+  ts_lds_barrier();
+  if (tid < 256) {  // the tile's 16 x 16 (m, row) outputs
+    const int l = tid >> 2, i = tid & 3;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc += red[(w * 64 + l) * 4 + i];
+    ys[(4 * (l >> 4) + i) * 17 + (l & 15)] = acc;
+  }
+  if (a.cap > 0) {
+    ts_lds_barrier();
+    // slot = col | (row in tile) << 32 | f16 delta << 48; a zero delta (an
+    // unused slot) adds nothing and is skipped
+    auto add_slot = [&](uint64_t v) {
+      const uint32_t dbits = (uint32_t)(v >> 48);
+      if (dbits == 0u) return;
+      const uint32_t col = (uint32_t)v, row = (uint32_t)(v >> 32) & 0xffffu;
+      const float d = ts_h2f((uint16_t)dbits);
+      for (int m = 0; m < a.M; ++m) {
+        const float xv = XLDS ? XT<BF16>::to_f(xs[m * a.K + col]) : XT<BF16>::to_f(a.x[(int64_t)m * a.ldx + col]);
+        atomicAdd(&ys[m * 17 + row], xv * d);
+      }
+    };
+    if (tid < a.cap) add_slot(slot0);
+    if (tid + NT < a.cap) add_slot(slot1);
+    for (int i = tid + 2 * NT; i < a.cap; i += NT) add_slot(a.slots[sbase + i]);  // rare: > 2 NT in a tile
+  }
+  ts_lds_barrier();
+  if (tid < 16 * a.M) {
+    const int m = tid >> 4, nn = tid & 15;
+    const int64_t r = r0 + nn;
+    if (r < a.N) {
+      float v = ys[m * 17 + nn];
+      if (a.bias_mul) v += XT<BF16>::to_f(bias_v);
+      const int64_t off = (int64_t)m * a.ldy + r;
+      if (a.y_dtype == TS_F32) reinterpret_cast<float*>(a.y)[off] = v;
+      else if (a.y_dtype == TS_BF16) reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2bf(v);
+      else reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2h(v);
+    }
+  }
+}
+
+template <int BITS, bool CB8, bool RVQ, int REP, int W>
+inline size_t decode_smem(int M, int64_t K, bool xlds) {
+  size_t s = 0;
+  if (BITS == 4) s += 256 * REP * 4;
+  if (BITS == 2 || RVQ) s += 256 * REP * 8;
+  if (BITS == 8 && CB8) s += 256 * REP * 4;
+  s += (size_t)W * 64 * 16;
+  s += 16 * 17 * 4;
+  s += 256 * 4;
+  s += 16;
+  if (xlds) s += ((size_t)M * K * 2 + 1023) / 1024 * 1024;  // whole 1 KB chunks
+  return s;
+}
+
+template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, bool XLDS, bool DQ, bool AL, int W, bool LOOP>
+inline int launch_decode_x(const DecodeArgs& a, hipStream_t st) {
+  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, W>(a.M, a.K, XLDS);
+  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XLDS, DQ, AL, W, LOOP>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess)
+      return TS_HIP_ERROR;
+    attr_set = true;
+  }
+  // one workgroup per 16-row tile; tiles beyond the resident capacity are
+  // scheduled by the hardware as workgroups retire
+  hipLaunchKernelGGL(kern, dim3((unsigned)a.n_tiles), dim3(64 * W), smem, st, a);
+  TS_CHECK_LAUNCH();
+  return TS_OK;
+}
+
+// Picks the variant: x staged in LDS when it fits, aligned metadata loads
+// when every batch is aligned, and the smallest workgroup (W waves per tile)
+// that leaves each wave at most two batches; the rest stream through the
+// looping kernel.
+template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP>
+inline int launch_decode(const DecodeArgs& a, hipStream_t st) {
+  constexpr int U = DecGeom<BITS, GS, RVQ>::U;
+  const bool xlds = (size_t)a.M * a.K * 2 <= DEC_XLDS_MAX;
+  const bool dq = a.dqsc != nullptr;
+  if (dq && a.dq_gs < (uint32_t)U) return TS_NOT_COVERED;  // a batch would span > 2 super-groups
+  // aligned: whole batches per row, and metadata base pointers aligned for
+  // U-wide (codes) / 2U-wide (f16) vector loads
+  auto aligned_ptr = [](const void* p, size_t al) { return (reinterpret_cast<uintptr_t>(p) % al) == 0; };
+  bool al = a.n_groups % U == 0;
+  if (dq) al = al && aligned_ptr(a.dqsc, U) && aligned_ptr(a.dqgc, U);
+  else al = al && aligned_ptr(a.scale, 2 * U) && aligned_ptr(a.gmin, 2 * U);
+  if (RVQ) al = al && aligned_ptr(a.s2scale, 2 * U) && aligned_ptr(a.s2gmin, 2 * U);
+  const int64_t T = (a.n_groups + U - 1) / U;  // batches per row
+#define TS_DEC(XL, DQV, ALV, WV, LP) return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XL, DQV, ALV, WV, LP>(a, st)
+#define TS_DEC_W(DQV)                              \
+  do {                                             \
+    if (xlds && al) {                              \
+      if (T <= 8) TS_DEC(true, DQV, true, 4, false);  \
+      if (T <= 16) TS_DEC(true, DQV, true, 8, false); \
+      if (T <= 32) TS_DEC(true, DQV, true, 16, false); \
+      TS_DEC(true, DQV, true, 16, true);           \
+    }                                              \
+    if (xlds) TS_DEC(true, DQV, false, 16, true);  \
+    if (al) TS_DEC(false, DQV, true, 16, true);    \
+    TS_DEC(false, DQV, false, 16, true);           \
+  } while (0)
+  if (dq) TS_DEC_W(true);
+  TS_DEC_W(false);
+#undef TS_DEC_W
+#undef TS_DEC
+}
+
+// Per-(bit width, group size) launchers, one translation unit each
+// (ts_decode_b<bits>_g<gs>.hip).
+int decode_b2_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b2_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b2_g256(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b4_g32(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b4_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b4_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b4_g256(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b6_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b6_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b8_g32(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b8_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b8_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+
+}  // namespace ts

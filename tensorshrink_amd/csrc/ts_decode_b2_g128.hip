@@ -1,0 +1,12 @@
+// Decode kernels for 2-bit layers (uniform or companded 4-level codebook); group size 128.
+// (One translation unit per bit width and group size keeps builds parallel.)
+#include "ts_decode.h"
+
+namespace ts {
+
+int decode_b2_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st) {
+  (void)L;
+  return bf16 ? launch_decode<2, 128, true, false, false, 4>(a, st) : launch_decode<2, 128, false, false, false, 4>(a, st);
+}
+
+}  // namespace ts

@@ -1,0 +1,12 @@
+// Decode kernels for 4-bit layers (uniform or NF4 / Lloyd-Max codebook); group size 256.
+// (One translation unit per bit width and group size keeps builds parallel.)
+#include "ts_decode.h"
+
+namespace ts {
+
+int decode_b4_g256(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st) {
+  (void)L;
+  return bf16 ? launch_decode<4, 256, true, false, false, 4>(a, st) : launch_decode<4, 256, false, false, false, 4>(a, st);
+}
+
+}  // namespace ts

@@ -1,0 +1,13 @@
+// Decode kernels for 6-bit layers: residual VQ, a 4-bit uniform stage plus a 2-bit uniform
+// residual stage, both applied in the same pass; group size 64.
+// (One translation unit per bit width and group size keeps builds parallel.)
+#include "ts_decode.h"
+
+namespace ts {
+
+int decode_b6_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st) {
+  (void)L;
+  return bf16 ? launch_decode<4, 64, true, false, true, 4>(a, st) : launch_decode<4, 64, false, false, true, 4>(a, st);
+}
+
+}  // namespace ts

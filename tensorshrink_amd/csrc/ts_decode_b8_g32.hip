@@ -1,0 +1,16 @@
+// Decode kernels for 8-bit layers: uniform codes (exact in bf16/f16 as integers) or a
+// 256-entry codebook (NF8) as a (hi, lo) pair of bf16/f16 values, so the
+// codebook value keeps ~16 mantissa bits; group size 32.
+// (One translation unit per bit width and group size keeps builds parallel.)
+#include "ts_decode.h"
+
+namespace ts {
+
+int decode_b8_g32(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st) {
+  (void)L;
+  if (L->codebook)
+    return bf16 ? launch_decode<8, 32, true, true, false, 16>(a, st) : launch_decode<8, 32, false, true, false, 16>(a, st);
+  return bf16 ? launch_decode<8, 32, true, false, false, 1>(a, st) : launch_decode<8, 32, false, false, false, 1>(a, st);
+}
+
+}  // namespace ts

@@ -49,6 +49,19 @@ struct PrefillArgs {
 
 constexpr int BK = 64;
 
+typedef __bf16 ts_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 ts_f16x2 __attribute__((ext_vector_type(2)));
+typedef float ts_f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed (lo, hi) bf16/f16 pair, round to nearest even
+// (v_cvt_pk_bf16_f32 on gfx950).
+template <bool BF16>
+TS_DEV uint32_t to_pair(float lo, float hi) {
+  const ts_f32x2 v = {lo, hi};
+  if constexpr (BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, ts_bf16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, ts_f16x2));
+}
+
 TS_DEV void pf_scale_gmin(const PrefillArgs& a, int64_t row, int64_t g, float& s, float& gm) {
   const int64_t flat = row * a.n_groups + g;
   if (a.dqsc) {
@@ -73,12 +86,15 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   constexpr int WB = CPT * BITS / 8;              // packed bytes per thread per k-step
   constexpr int WB2 = CPT / 4;                    // RVQ stage-2 bytes
   constexpr int CBN = (CB && BITS == 8) ? 256 : 16;
+  constexpr int OMAX = 8;                         // outliers per row staged in LDS
   static_assert(CPT % 32 == 0 || CPT == 16, "weight chunk");
   static_assert(WB % 4 == 0, "packed chunk");
   extern __shared__ __align__(16) unsigned char smem[];
   uint16_t* As = reinterpret_cast<uint16_t*>(smem);             // [2][BM][64]
   uint16_t* Bs = As + 2 * BM * BK;                              // [2][BN][64]
   float* cbs = reinterpret_cast<float*>(Bs + 2 * BN * BK);      // codebook
+  int32_t* ocs = reinterpret_cast<int32_t*>(cbs + CBN);         // [BN][OMAX] outlier columns of each tile row
+  float* ods = reinterpret_cast<float*>(ocs + BN * OMAX);       // [BN][OMAX] outlier deltas
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -107,6 +123,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const uint8_t* wp2 = RVQ ? a.s2packed + wrow * a.s2stride + (wpart * CPT) / 4 : nullptr;
   const int32_t o_begin = a.orow_ptr ? a.orow_ptr[wrow] : 0;
   const int32_t o_end = (a.orow_ptr && n0 + wr < a.N) ? a.orow_ptr[wrow + 1] : o_begin;
+  const int o_cnt = (int)(o_end - o_begin);
+  if (wpart == 0) {
+    for (int i = 0; i < OMAX && i < o_cnt; ++i) {
+      ocs[wr * OMAX + i] = a.ocol[o_begin + i];
+      ods[wr * OMAX + i] = ts_h2f(a.odelta[o_begin + i]);
+    }
+  }
 
   ts_u32x4 areg[A_CHUNKS];
   uint32_t wreg[WB / 4];
@@ -124,8 +147,16 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       areg[i] = (m < a.M && col < a.cols) ? ts_ld16(a.x + m * a.ldx + col) : ts_u32x4{0u, 0u, 0u, 0u};
     }
     const uint8_t* p = wp + (k0 * BITS) / 8;
+    if constexpr (WB % 16 == 0) {
 #pragma unroll
-    for (int i = 0; i < WB / 4; ++i) wreg[i] = ts_ld4(p + 4 * i);
+      for (int i = 0; i < WB / 16; ++i) {
+        const ts_u32x4 v = ts_ld16(p + 16 * i);
+        wreg[4 * i] = v.x; wreg[4 * i + 1] = v.y; wreg[4 * i + 2] = v.z; wreg[4 * i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < WB / 4; ++i) wreg[i] = ts_ld4(p + 4 * i);
+    }
     if constexpr (RVQ) {
       const uint8_t* p2 = wp2 + k0 / 4;
 #pragma unroll
@@ -155,41 +186,73 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
     // dequantize CPT codes of row wr, 8 at a time (one 16-byte chunk)
 #pragma unroll
     for (int c8 = 0; c8 < CPT / 8; ++c8) {
-      const int sc = (c8 * 8) / 32;
-      const float s = sreg[CPT >= 32 ? sc : 0][0], gm = sreg[CPT >= 32 ? sc : 0][1];
+      const int sc = CPT >= 32 ? (c8 * 8) / 32 : 0;
+      const float s = sreg[sc][0], gm = sreg[sc][1];
+      float cv[8];
+      if constexpr (BITS == 4) {
+        // one dword = 8 codes; spread even/odd nibbles into bytes
+        const uint32_t d = wreg[c8];
+        if constexpr (CB) {
+          const uint32_t lo = (d << 2) & 0x3c3c3c3cu, hi = (d >> 2) & 0x3c3c3c3cu;  // 4*code per byte
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            cv[2 * e] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cbs) + ((lo >> (8 * e)) & 0xffu));
+            cv[2 * e + 1] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cbs) + ((hi >> (8 * e)) & 0xffu));
+          }
+        } else {
+          const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            cv[2 * e] = (float)((lo >> (8 * e)) & 0xffu);
+            cv[2 * e + 1] = (float)((hi >> (8 * e)) & 0xffu);
+          }
+        }
+      } else if constexpr (BITS == 2) {
+        const uint32_t d = wreg[c8 >> 1] >> (16 * (c8 & 1));  // 8 codes in 16 bits
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t c = (d >> (2 * e)) & 3u;
+          cv[e] = CB ? cbs[c] : (float)c;
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t d = wreg[2 * c8 + h];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t c = (d >> (8 * e)) & 0xffu;
+            cv[4 * h + e] = CB ? cbs[c] : (float)c;
+          }
+        }
+      }
       float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int ci = c8 * 8 + e;  // code index within the thread's chunk
-        uint32_t code;
-        if constexpr (BITS == 4) code = (wreg[ci >> 3] >> (4 * (ci & 7))) & 15u;
-        else if constexpr (BITS == 2) code = (wreg[ci >> 4] >> (2 * (ci & 15))) & 3u;
-        else code = (wreg[ci >> 2] >> (8 * (ci & 3))) & 255u;
-        const float cv = CB ? cbs[code] : (float)code;
-        float w = __builtin_fmaf(cv, s, gm);
-        if constexpr (RVQ) {
-          const uint32_t c2 = (wreg2[ci >> 4] >> (2 * (ci & 15))) & 3u;
-          w += __builtin_fmaf((float)c2, sreg[CPT >= 32 ? sc : 0][2], sreg[CPT >= 32 ? sc : 0][3]);
-        }
-        v[e] = w;
+      for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(cv[e], s, gm);
+      if constexpr (RVQ) {
+        const float s2 = sreg[sc][2], g2 = sreg[sc][3];
+        const uint32_t d2 = wreg2[c8 >> 1] >> (16 * (c8 & 1));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += __builtin_fmaf((float)((d2 >> (2 * e)) & 3u), s2, g2);
       }
       ts_u32x4 pk;
-      pk.x = (uint32_t)XT<BF16>::from_f(v[0]) | ((uint32_t)XT<BF16>::from_f(v[1]) << 16);
-      pk.y = (uint32_t)XT<BF16>::from_f(v[2]) | ((uint32_t)XT<BF16>::from_f(v[3]) << 16);
-      pk.z = (uint32_t)XT<BF16>::from_f(v[4]) | ((uint32_t)XT<BF16>::from_f(v[5]) << 16);
-      pk.w = (uint32_t)XT<BF16>::from_f(v[6]) | ((uint32_t)XT<BF16>::from_f(v[7]) << 16);
+      pk.x = to_pair<BF16>(v[0], v[1]);
+      pk.y = to_pair<BF16>(v[2], v[3]);
+      pk.z = to_pair<BF16>(v[4], v[5]);
+      pk.w = to_pair<BF16>(v[6], v[7]);
       const int chunk = (wpart * CPT) / 8 + c8;
       *reinterpret_cast<ts_u32x4*>(Bb + swz(wr, chunk)) = pk;
     }
     // fold this row's outliers that land in the k-step into the tile
-    if (o_end > o_begin) {
+    if (o_cnt > 0) {
       const int64_t kc0 = kt * BK + wpart * CPT;
-      for (int32_t o = o_begin; o < o_end; ++o) {
-        const int64_t col = a.ocol[o];
+      const int nl = o_cnt < OMAX ? o_cnt : OMAX;
+      for (int i = 0; i < o_cnt; ++i) {
+        const int64_t col = i < nl ? ocs[wr * OMAX + i] : a.ocol[o_begin + i];
         if (col >= kc0 && col < kc0 + CPT) {
+          const float dl = i < nl ? ods[wr * OMAX + i] : ts_h2f(a.odelta[o_begin + i]);
           const int kk = (int)(col - kt * BK);
           uint16_t* p = Bb + swz(wr, kk >> 3) + (kk & 7);
-          *p = XT<BF16>::from_f(XT<BF16>::to_f(*p) + ts_h2f(a.odelta[o]));
+          *p = XT<BF16>::from_f(XT<BF16>::to_f(*p) + dl);
         }
       }
     }
@@ -258,7 +321,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
 template <int BITS, int GS, bool BF16, bool CB, bool RVQ, int BM, int BN>
 static int launch_prefill(PrefillArgs a, hipStream_t st) {
   constexpr int CBN = (CB && BITS == 8) ? 256 : 16;
-  const size_t smem = (size_t)2 * (BM + BN) * BK * 2 + CBN * 4;
+  const size_t smem = (size_t)2 * (BM + BN) * BK * 2 + CBN * 4 + (size_t)BN * 8 * 8;
   auto kern = prefill_kernel<BITS, GS, BF16, CB, RVQ, BM, BN>;
   static bool attr_set = false;
   if (!attr_set) {

@@ -29,6 +29,25 @@ def _row_ptr(outlier_row: torch.Tensor, rows: int) -> torch.Tensor:
     return rp
 
 
+def tile_outlier_slots(row_ptr: torch.Tensor, outlier_row: torch.Tensor, outlier_col: torch.Tensor,
+                       outlier_delta: torch.Tensor, rows: int):
+    """Per-16-row-tile outlier slots for the decode kernel (ts_build_tile_outliers):
+    returns (slots u64 as int64 [n_tiles * cap], cap). cap is the largest
+    per-tile count rounded up to a multiple of 8; reading it back syncs the
+    stream, so QuantLinear builds the table once at construction."""
+    dev = row_ptr.device
+    lib = L.lib()
+    mx = torch.empty(1, dtype=torch.int32, device=dev)
+    L.check(lib.ts_tile_outlier_max(row_ptr.data_ptr(), rows, mx.data_ptr(), L.stream_ptr(dev)), "tile outlier count")
+    cap = max(8, (int(mx.item()) + 7) // 8 * 8)
+    n_tiles = (rows + 15) // 16
+    slots = torch.empty(n_tiles * cap, dtype=torch.int64, device=dev)
+    L.check(lib.ts_build_tile_outliers(row_ptr.data_ptr(), outlier_row.data_ptr(), outlier_col.data_ptr(),
+                                       outlier_delta.data_ptr(), rows, cap, slots.data_ptr(), L.stream_ptr(dev)),
+            "tile outlier slots")
+    return slots, cap
+
+
 def fused_quantized_linear(
     x: torch.Tensor, packed: torch.Tensor, scale: Optional[torch.Tensor], gmin: Optional[torch.Tensor],
     bias: Optional[torch.Tensor], bits: int, group_size: int, cols: int, out_features: int,
@@ -71,12 +90,15 @@ def fused_quantized_linear(
     if stage2_packed is not None:
         s.stage2_packed, s.stage2_stride = stage2_packed.data_ptr(), stage2_packed.shape[1]
         s.stage2_scale, s.stage2_gmin = stage2_scale.data_ptr(), stage2_gmin.data_ptr()
-    rp = None
+    rp = slots = None
     if outlier_row is not None and outlier_row.numel() > 0:
         rp = _row_ptr(outlier_row, out_features)
         s.outlier_row, s.outlier_col = outlier_row.data_ptr(), outlier_col.data_ptr()
         s.outlier_delta, s.n_outliers = outlier_delta.data_ptr(), outlier_row.numel()
         s.outlier_row_ptr = rp.data_ptr()
+        if M <= 16:  # the decode kernel reads outliers per tile
+            slots, cap = tile_outlier_slots(rp, outlier_row, outlier_col, outlier_delta, out_features)
+            s.tile_outliers, s.tile_outlier_cap = slots.data_ptr(), cap
     ydt = torch.float32 if return_fp32 else compute_dtype
     if out is None or out.shape != (M, out_features) or out.dtype != ydt or not out.is_contiguous():
         out = torch.empty(M, out_features, dtype=ydt, device=x.device)

@@ -11,6 +11,9 @@ correction and bias fused; there is no CPU or PyTorch fallback path.
 Additions over the reference:
   * ``outlier_row_ptr`` - non-persistent int32 [rows + 1] CSR offsets into the
     row-sorted outlier tables (derived data, absent from state_dict);
+  * ``tile_outliers`` - non-persistent per-16-row-tile outlier slots (u64:
+    col, row in tile, f16 delta; ``tile_outlier_cap`` slots per tile) that
+    the decode kernel reads at a fixed address (derived data);
   * 6-bit RVQ layers register ``stage2_packed``, ``stage2_scale`` and
     ``stage2_gmin`` (the reference QuantLinear cannot serve bits=6).
 ``WeightCache`` (a dense-weight cache) is not part of this path: passing
@@ -124,6 +127,14 @@ class QuantLinear(nn.Module):
         self.register_buffer("outlier_col", ocol)
         self.register_buffer("outlier_delta", odelta)
         self.register_buffer("outlier_row_ptr", rptr, persistent=False)
+        # derived per-tile slots for the decode kernel (fixed-address loads)
+        if n > 0:
+            from .kernels import tile_outlier_slots
+            with torch.cuda.device(dev):
+                slots, self.tile_outlier_cap = tile_outlier_slots(rptr, orow, ocol, odelta, self.rows)
+        else:
+            slots, self.tile_outlier_cap = torch.zeros(0, dtype=torch.int64, device=dev), 0
+        self.register_buffer("tile_outliers", slots, persistent=False)
         if bias is not None:
             self.register_buffer("bias", bias.detach().clone().to(dev))
         else:
@@ -161,6 +172,9 @@ class QuantLinear(nn.Module):
             s.outlier_delta = self.outlier_delta.data_ptr()
             s.n_outliers = self.outlier_row.numel()
             s.outlier_row_ptr = self.outlier_row_ptr.data_ptr()
+            if self.tile_outlier_cap > 0:
+                s.tile_outliers = self.tile_outliers.data_ptr()
+                s.tile_outlier_cap = self.tile_outlier_cap
         return s
 
     def _rebuild_cache(self) -> None:
