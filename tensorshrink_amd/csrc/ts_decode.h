@@ -79,6 +79,8 @@ struct DecodeArgs {
 };
 
 constexpr size_t DEC_XLDS_MAX = 32 * 1024;  // activations staged in LDS up to this size
+enum { XM_GLOBAL = 0, XM_DMA = 1, XM_REG = 2 };
+constexpr int XREG_CHUNKS = 2;  // 16-byte x chunks per thread with XM_REG
 
 template <bool BF16>
 TS_DEV uint32_t pack2(float lo, float hi) {
@@ -125,26 +127,37 @@ struct DecGeom {
   static constexpr int GB2 = GS / 4;        // RVQ stage-2 bytes per row per group
   static constexpr int LB2 = GB2 / 4;
   static constexpr int U0 = (LB + (RVQ ? LB2 : 0)) > 0 ? 64 / (LB + (RVQ ? LB2 : 0)) : 8;
-  // groups per batch (~64 B of codes per lane), a power of two in [1, 8]
-  static constexpr int U = U0 >= 8 ? 8 : (U0 >= 4 ? 4 : (U0 >= 2 ? 2 : 1));
+  // largest groups per batch (~64 B of codes per lane), a power of two in [1, 8]
+  static constexpr int UMAX = U0 >= 8 ? 8 : (U0 >= 4 ? 4 : (U0 >= 2 ? 2 : 1));
 };
 
 // W: waves per workgroup (4, 8 or 16), all on the same tile, each owning a
-// contiguous run of its group batches. Without LOOP every wave has at most
-// two batches and the kernel is straight-line code: the host picks the
-// smallest W for which that holds. LOOP streams longer runs through the two
-// register buffers.
+// contiguous run of its batches of U groups. Without LOOP every wave has at
+// most two batches and the kernel is straight-line code. The host spreads a
+// tile over more waves (smaller U) when there are few tiles, so a small layer
+// still has several waves per SIMD to hide LDS and MFMA latency. LOOP streams
+// longer runs through the two register buffers.
+// XM: where the A operand (x) comes from: XM_GLOBAL reads it from global
+// memory per MFMA (x too large for LDS); XM_REG stages it in LDS through
+// registers (at most XREG_CHUNKS 16-byte chunks per thread); XM_DMA stages it
+// with direct global->LDS loads. XM_REG keeps the compiler's wait counts
+// exact, so a wave computes its first batch while the second is in flight;
+// with direct-to-LDS loads pending the compiler treats the load counter as
+// out of order and its first wait drains everything.
 // AL: the row's group count is a multiple of U, so every batch starts on a
 // multiple of U in the row-major (row, group) metadata arrays and its U codes
 // / scales come in one aligned vector load.
 // Occupancy: at most 128 VGPRs (4 waves per SIMD, 16 per CU), so 1024 waves
 // of 16-row tiles are resident at once across 256 CUs.
-template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, bool XLDS, bool DQ, bool AL, int W, bool LOOP>
+template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
+          bool LOOP>
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in) {
   constexpr int NT = 64 * W;
+  constexpr bool XLDS = XM != XM_GLOBAL;
   extern __shared__ __align__(16) unsigned char smem[];
   using Geo = DecGeom<BITS, GS, RVQ>;
-  constexpr int GB = Geo::GB, LB = Geo::LB, GB2 = Geo::GB2, LB2 = Geo::LB2, U = Geo::U;
+  constexpr int GB = Geo::GB, LB = Geo::LB, GB2 = Geo::GB2, LB2 = Geo::LB2;
+  static_assert(U >= 1 && U <= Geo::UMAX && (U & (U - 1)) == 0, "groups per batch");
   constexpr int NMF = (BITS == 8 && CB8) ? GS / 16 : GS / 32;  // MFMAs per group
   constexpr int CPM = (BITS == 8 && CB8) ? 4 : 8;              // codes per lane per MFMA
   constexpr bool USE_T4 = (BITS == 4);
@@ -190,8 +203,6 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   sp += 16 * 17 * 4;
   float* cbs = reinterpret_cast<float*>(sp);       // [256] staged codebook
   sp += 256 * 4;
-  uint32_t* xzero = reinterpret_cast<uint32_t*>(sp);  // 16 zero bytes: x rows >= M read here
-  sp += 16;
   uint16_t* xs = reinterpret_cast<uint16_t*>(sp);  // [M][K] staged activations (XLDS)
 
   // ---- per-wave share of every tile ----------------------------------------
@@ -203,7 +214,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   const int g_lo = U * ((T * wave) / W);
   const int g_hi = min(G, U * ((T * (wave + 1)) / W));
   const int nb = (T + W - 1) / W;
-  const bool xrow = n < a.M;
+  const uint16_t* xrow_lds = xs + min(n, a.M - 1) * a.K;          // this lane's x row (staged)
+  const uint16_t* xrow_glb = a.x + (int64_t)min(n, a.M - 1) * a.ldx;  // this lane's x row (global)
   constexpr uint32_t ONE = XT<BF16>::ONE;
   const ts_u32x4 ones = CB8 ? ts_u32x4{ONE, ONE, ONE, ONE}
                             : ts_u32x4{ONE | (ONE << 16), ONE | (ONE << 16), ONE | (ONE << 16), ONE | (ONE << 16)};
@@ -314,22 +326,22 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
 #pragma unroll
       for (int j = 0; j < NMF; ++j) {
         const int col = c0 + j * CPM;
+        // A-operand row n >= M only feeds output rows that are never stored,
+        // so those lanes read row M - 1 (no predicate, one base per lane).
         if constexpr (CPM == 8) {
           if constexpr (XLDS) {
-            const void* xp = xrow ? static_cast<const void*>(xs + n * a.K + col) : static_cast<const void*>(xzero);
-            xa[j] = *reinterpret_cast<const ts_u32x4*>(xp);
+            xa[j] = *reinterpret_cast<const ts_u32x4*>(xrow_lds + col);
           } else {
-            const ts_u32x4 v = ts_ld16(a.x + min(n, a.M - 1) * a.ldx + min(col, (int)a.cols - 8));
-            xa[j] = (xrow && col < a.cols) ? v : ts_u32x4{0u, 0u, 0u, 0u};
+            const ts_u32x4 v = ts_ld16(xrow_glb + min(col, (int)a.cols - 8));
+            xa[j] = col < a.cols ? v : ts_u32x4{0u, 0u, 0u, 0u};
           }
         } else {
           ts_u32x2 v;
           if constexpr (XLDS) {
-            const void* xp = xrow ? static_cast<const void*>(xs + n * a.K + col) : static_cast<const void*>(xzero);
-            v = *reinterpret_cast<const ts_u32x2*>(xp);
+            v = *reinterpret_cast<const ts_u32x2*>(xrow_lds + col);
           } else {
-            const ts_u32x2 l = ts_ld8(a.x + min(n, a.M - 1) * a.ldx + min(col, (int)a.cols - 4));
-            v = (xrow && col < a.cols) ? l : ts_u32x2{0u, 0u};
+            const ts_u32x2 l = ts_ld8(xrow_glb + min(col, (int)a.cols - 4));
+            v = col < a.cols ? l : ts_u32x2{0u, 0u};
           }
           // (x_k, x_k) pairs so one (hi, lo) table word multiplies x_k twice.
           xa[j] = ts_u32x4{__builtin_amdgcn_perm(v.x, v.x, 0x05040100u), __builtin_amdgcn_perm(v.x, v.x, 0x07060302u),
@@ -366,7 +378,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
           bv2[j] = ts_u32x4{e0.x, e0.y, e1.x, e1.y};
         }
       }
-      // Phase 2: the group's MFMAs.
+      // Phase 2: the group's MFMAs (ax: per-row sums of x over the group).
       ts_f32x4 aw = {0.f, 0.f, 0.f, 0.f};
       ts_f32x4 ax = {0.f, 0.f, 0.f, 0.f};
       ts_f32x4 aw2 = {0.f, 0.f, 0.f, 0.f};
@@ -404,19 +416,19 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   // Every load of the tile is issued up front, none depending on another: x
   // chunks, the codebook, both weight batches, the tile's outlier slots and
   // the bias.
-  // x -> LDS ([M][K] bf16/f16) with direct global->LDS loads: each wave
-  // instruction moves one 1 KB chunk (16 B per lane, lane-contiguous), so no
-  // registers are held while the weight loads are issued. Lanes past the
-  // end of x read a clamped (valid) address; their bytes land in the padded
-  // tail of the buffer or in the column padding, which is zeroed below.
+  // x -> LDS ([M][K] bf16/f16).
+  // XM_DMA: direct global->LDS loads, each wave instruction moving one 1 KB
+  // chunk (16 B per lane, lane-contiguous). Lanes past the end of x read a
+  // clamped (valid) address; their bytes land in the padded tail of the
+  // buffer or in the column padding, which is zeroed below. The issue loop is
+  // unrolled to a compile-time bound with uniform predicates.
+  // XM_REG: XREG_CHUNKS 16-byte chunks per thread into registers, stored to
+  // LDS once every load of the tile is issued.
   // (32-bit arithmetic: with x staged, M * K * 2 <= DEC_XLDS_MAX.)
   const uint32_t kK = (uint32_t)a.K;
-  const uint32_t xchunks = XLDS ? ((uint32_t)a.M * kK * 2u + 1023u) / 1024u : 0u;
-  // (unrolled to a compile-time bound with uniform predicates: a loop with a
-  // runtime trip count would hide from the compiler how many loads follow
-  // each one, and every later wait would become a full drain)
-  constexpr int XCW = XLDS ? (int)((DEC_XLDS_MAX / 1024 + W - 1) / W) : 0;  // max chunks per wave
-  if constexpr (XLDS) {
+  const uint32_t xchunks = XM == XM_DMA ? ((uint32_t)a.M * kK * 2u + 1023u) / 1024u : 0u;
+  constexpr int XCW = XM == XM_DMA ? (int)((DEC_XLDS_MAX / 1024 + W - 1) / W) : 0;  // max chunks per wave
+  if constexpr (XM == XM_DMA) {
 #pragma unroll
     for (int i = 0; i < XCW; ++i) {
       const uint32_t c = (uint32_t)(wave + i * W);
@@ -427,6 +439,18 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
         __builtin_amdgcn_global_load_lds(a.x + (int64_t)m * a.ldx + k,
                                          (__attribute__((address_space(3))) void*)(xs + c * 512u), 16, 0, 0);
       }
+    }
+  }
+  const uint32_t kch = kK / 8u;                                   // 16-byte chunks per x row
+  const uint32_t xch8 = XM == XM_REG ? (uint32_t)a.M * kch : 1u;  // chunks of x
+  ts_u32x4 xr[XM == XM_REG ? XREG_CHUNKS : 1];
+  if constexpr (XM == XM_REG) {
+#pragma unroll
+    for (int i = 0; i < XREG_CHUNKS; ++i) {
+      const uint32_t c = min((uint32_t)(tid + i * NT), xch8 - 1u);
+      const uint32_t m = c / kch;
+      const uint32_t k = min((c - m * kch) * 8u, (uint32_t)a.cols - 8u);
+      xr[i] = ts_ld16(a.x + (int64_t)m * a.ldx + k);
     }
   }
   constexpr int NCB = 1 << (RVQ ? 4 : BITS);
@@ -450,8 +474,18 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   // slot tid % 256): a store under `tid < NCB` would let the compiler sink
   // the codebook load next to it and wait there for every load issued before.
   cbs[cbi] = a.cb_is_table ? cbraw : (float)cbi;
-  if (tid < 4) xzero[tid] = 0u;
-  if constexpr (XLDS) {
+  if constexpr (XM == XM_REG) {
+    // unconditional stores (a thread past the end rewrites the last chunk
+    // with the same bytes): a store under a predicate would let the compiler
+    // sink its load next to it, past the weight loads, and drain them there
+#pragma unroll
+    for (int i = 0; i < XREG_CHUNKS; ++i) {
+      const uint32_t c = min((uint32_t)(tid + i * NT), xch8 - 1u);
+      const uint32_t m = c / kch, k = (c - m * kch) * 8u;
+      *reinterpret_cast<ts_u32x4*>(xs + m * kK + k) = k < (uint32_t)a.cols ? xr[i] : ts_u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  if constexpr (XM == XM_DMA) {
     // Each wave waits for its own chunks before the barrier (reading one word
     // of the last one back makes the compiler emit the wait). The compiler's
     // wait-count model treats direct-to-LDS loads as completing out of order
@@ -567,15 +601,15 @@ inline size_t decode_smem(int M, int64_t K, bool xlds) {
   s += (size_t)W * 64 * 16;
   s += 16 * 17 * 4;
   s += 256 * 4;
-  s += 16;
   if (xlds) s += ((size_t)M * K * 2 + 1023) / 1024 * 1024;  // whole 1 KB chunks
   return s;
 }
 
-template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, bool XLDS, bool DQ, bool AL, int W, bool LOOP>
+template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
+          bool LOOP>
 inline int launch_decode_x(const DecodeArgs& a, hipStream_t st) {
-  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, W>(a.M, a.K, XLDS);
-  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XLDS, DQ, AL, W, LOOP>;
+  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, W>(a.M, a.K, XM != XM_GLOBAL);
+  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, LOOP>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -590,40 +624,74 @@ inline int launch_decode_x(const DecodeArgs& a, hipStream_t st) {
   return TS_OK;
 }
 
+// Shape of a launch: W waves per tile, U groups per batch.
+struct DecShape {
+  int W, U;
+  bool ok;
+};
+
+// U is the largest batch (fewest loads per payload byte). W: the smallest in
+// {4, 8, 16} that covers a row in two batches per wave, raised (fewer batches
+// per wave, so less serial compute per wave) while the launch stays within
+// one resident round of 4096 waves (16 per CU at <= 128 VGPRs) and no wave
+// would be idle. ok == false: the row is too long, stream it (LOOP).
+inline DecShape decode_shape(int64_t n_tiles, int64_t G, int umax) {
+  const int64_t T = (G + umax - 1) / umax;  // batches per row
+  int w = 4;
+  while (w < 16 && (T + w - 1) / w > 2) w *= 2;
+  if ((T + w - 1) / w > 2) return {16, umax, false};
+  while (w < 16 && 2 * w <= T && n_tiles * 2 * w <= 4096) w *= 2;
+  return {w, umax, true};
+}
+
 // Picks the variant: x staged in LDS when it fits, aligned metadata loads
-// when every batch is aligned, and the smallest workgroup (W waves per tile)
-// that leaves each wave at most two batches; the rest stream through the
-// looping kernel.
+// when every batch is aligned, and the straight-line shape above; the rest
+// (x too large for LDS, unaligned metadata, rows longer than 32 batches of
+// the largest U) stream through the looping kernel.
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP>
 inline int launch_decode(const DecodeArgs& a, hipStream_t st) {
-  constexpr int U = DecGeom<BITS, GS, RVQ>::U;
+  constexpr int UMAX = DecGeom<BITS, GS, RVQ>::UMAX;
   const bool xlds = (size_t)a.M * a.K * 2 <= DEC_XLDS_MAX;
   const bool dq = a.dqsc != nullptr;
-  if (dq && a.dq_gs < (uint32_t)U) return TS_NOT_COVERED;  // a batch would span > 2 super-groups
-  // aligned: whole batches per row, and metadata base pointers aligned for
-  // U-wide (codes) / 2U-wide (f16) vector loads
+  if (dq && a.dq_gs < (uint32_t)UMAX) return TS_NOT_COVERED;  // a batch would span > 2 super-groups
   auto aligned_ptr = [](const void* p, size_t al) { return (reinterpret_cast<uintptr_t>(p) % al) == 0; };
-  bool al = a.n_groups % U == 0;
-  if (dq) al = al && aligned_ptr(a.dqsc, U) && aligned_ptr(a.dqgc, U);
-  else al = al && aligned_ptr(a.scale, 2 * U) && aligned_ptr(a.gmin, 2 * U);
-  if (RVQ) al = al && aligned_ptr(a.s2scale, 2 * U) && aligned_ptr(a.s2gmin, 2 * U);
-  const int64_t T = (a.n_groups + U - 1) / U;  // batches per row
-#define TS_DEC(XL, DQV, ALV, WV, LP) return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XL, DQV, ALV, WV, LP>(a, st)
-#define TS_DEC_W(DQV)                              \
-  do {                                             \
-    if (xlds && al) {                              \
-      if (T <= 8) TS_DEC(true, DQV, true, 4, false);  \
-      if (T <= 16) TS_DEC(true, DQV, true, 8, false); \
-      if (T <= 32) TS_DEC(true, DQV, true, 16, false); \
-      TS_DEC(true, DQV, true, 16, true);           \
-    }                                              \
-    if (xlds) TS_DEC(true, DQV, false, 16, true);  \
-    if (al) TS_DEC(false, DQV, true, 16, true);    \
-    TS_DEC(false, DQV, false, 16, true);           \
+  // aligned for batches of u groups: whole batches per row, and metadata base
+  // pointers aligned for u-wide (codes) / 2u-wide (f16) vector loads
+  auto aligned = [&](int u) {
+    bool al = a.n_groups % u == 0;
+    if (dq) al = al && aligned_ptr(a.dqsc, u) && aligned_ptr(a.dqgc, u);
+    else al = al && aligned_ptr(a.scale, 2 * u) && aligned_ptr(a.gmin, 2 * u);
+    if (RVQ) al = al && aligned_ptr(a.s2scale, 2 * u) && aligned_ptr(a.s2gmin, 2 * u);
+    return al;
+  };
+  const DecShape sh = decode_shape(a.n_tiles, a.n_groups, UMAX);
+  // x through registers when XREG_CHUNKS chunks per thread hold it
+  auto xreg = [&](int w) { return xlds && (int64_t)a.M * a.K / 8 <= (int64_t)XREG_CHUNKS * 64 * w; };
+#define TS_DEC(XMV, DQV, ALV, WV, UV, LP) \
+  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, LP>(a, st)
+#define TS_DEC_ALL(DQV)                                                          \
+  do {                                                                           \
+    const bool alm = aligned(UMAX);                                              \
+    if (xlds && sh.ok && alm) {                                                  \
+      if (sh.W == 4) {                                                           \
+        if (xreg(4)) TS_DEC(XM_REG, DQV, true, 4, UMAX, false);                  \
+        TS_DEC(XM_DMA, DQV, true, 4, UMAX, false);                               \
+      }                                                                          \
+      if (sh.W == 8) {                                                           \
+        if (xreg(8)) TS_DEC(XM_REG, DQV, true, 8, UMAX, false);                  \
+        TS_DEC(XM_DMA, DQV, true, 8, UMAX, false);                               \
+      }                                                                          \
+      if (xreg(16)) TS_DEC(XM_REG, DQV, true, 16, UMAX, false);                  \
+      TS_DEC(XM_DMA, DQV, true, 16, UMAX, false);                                \
+    }                                                                            \
+    if (xlds && alm) TS_DEC(XM_DMA, DQV, true, 16, UMAX, true);                  \
+    if (xlds) TS_DEC(XM_DMA, DQV, false, 16, UMAX, true);                        \
+    if (alm) TS_DEC(XM_GLOBAL, DQV, true, 16, UMAX, true);                       \
+    TS_DEC(XM_GLOBAL, DQV, false, 16, UMAX, true);                               \
   } while (0)
-  if (dq) TS_DEC_W(true);
-  TS_DEC_W(false);
-#undef TS_DEC_W
+  if (dq) TS_DEC_ALL(true);
+  TS_DEC_ALL(false);
+#undef TS_DEC_ALL
 #undef TS_DEC
 }
 
