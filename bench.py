@@ -128,41 +128,72 @@ def bench_decode(args, opts):
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     gpu_ms = [a.elapsed_time(b) for a, b in evs[1:]]  # the first pair starts on an idle queue
     step_gpu_ms = sum(gpu_ms) / len(gpu_ms)
-    achieved = step_bytes / (step_gpu_ms * 1e-3) / 1e9
-    detail = per_linear_detail(base, xs, stream)
-    return dict(ms_per_step=ms_per_step, value=value, step_bytes=step_bytes, achieved=achieved, detail=detail,
+    kern = per_linear_kernel_time(copies, xs, stream, reps=args.kernel_reps)
+    return dict(ms_per_step=ms_per_step, value=value, step_bytes=step_bytes, kern=kern,
                 base=base, xs=xs, step_gpu_us=step_gpu_ms * 1e3)
 
 
-def per_linear_detail(base, xs, stream, reps: int = 20):
-    """Per-linear decode launch times: eager launches with events, queued
-    behind a long matmul so the host's launch overhead never idles the GPU.
-    The copies rotate so no launch finds its weights in the MALL."""
-    big = torch.randn(12288, 12288, device="cuda", dtype=torch.bfloat16)
-    times = {name: [] for name, _ in base}
+def per_linear_kernel_time(copies, xs, stream, reps: int):
+    """Average decode-kernel launch duration per linear: one graph per linear
+    position holding that linear's launch on every copy (back to back, the
+    weights rotating so none comes from the MALL), replayed `reps` times
+    between two HIP events on the launch stream. The per-launch average
+    includes the dispatch gap between consecutive kernels of a graph."""
+    out = {}
     with torch.cuda.stream(stream):
+        graphs = []
+        for p, (name, q0) in enumerate(copies[0]):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for layer in copies:
+                    layer[p][1](xs[q0.in_features])
+            graphs.append((name, q0, g))
+        for _, _, g in graphs:
+            g.replay()
         torch.cuda.synchronize()
-        for _ in range(3):
-            big = (big @ big).clamp_(-1, 1)  # ~10 ms of queued work
         evs = []
-        for r in range(reps):
-            for name, q in base:
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record(stream)
-                q(xs[q.in_features])
-                b.record(stream)
-                evs.append((name, a, b))
+        for name, q0, g in graphs:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(stream)
+            evs.append((name, q0, e0, e1))
         torch.cuda.synchronize()
-    for name, a, b in evs:
-        times[name].append(a.elapsed_time(b))
-    detail = {}
-    for name, q in base:
-        t = sorted(times[name])[: max(1, len(times[name]) // 2)]  # faster half: weights cold in HBM vs MALL
-        avg = sum(t) / len(t)
-        nb = layer_bytes(q, 1)
-        detail[name] = {"shape": [q.out_features, q.in_features], "bytes": nb, "us": round(avg * 1e3, 2),
-                        "GBps": round(nb / (avg * 1e-3) / 1e9, 1)}
-    return detail
+    for name, q0, e0, e1 in evs:
+        us = e0.elapsed_time(e1) * 1e3 / (reps * len(copies))
+        nb = layer_bytes(q0, 1)
+        out[name] = {"shape": [q0.out_features, q0.in_features], "bytes": nb, "us": round(us, 2),
+                     "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
+    return out
+
+
+def load_traffic(detail):
+    """HBM bytes per launch from the committed PMC summary (FETCH_SIZE and
+    WRITE_SIZE passes of rocprofv3 over this bench, each scaled by the same
+    counter's reading for a plain copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        t = json.load(open(path))
+        per = t["per_linear_bytes"]
+        return {"bytes_per_step": int(sum(per[n] for n in detail)),
+                "per_linear_bytes": {n: int(per[n]) for n in detail},
+                "source": "profiles/decode_traffic.json"}
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_calibration():
+    """A plain device copy of known size, for scaling FETCH_SIZE/WRITE_SIZE."""
+    n = 512 * 1024 * 1024
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
 
 
 def bench_prefill(args):
@@ -262,6 +293,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=10)
+    ap.add_argument("--copy-calib", action="store_true", help="only run the plain-copy PMC calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build targets a single MI355X and has no multi-GPU path "
@@ -269,10 +302,18 @@ def main():
         sys.exit(2)
     import tensorshrink_amd  # noqa: F401  (fails loudly without the built library)
     torch.cuda.set_device(0)
+    if args.copy_calib:
+        copy_calibration()
+        return
     opts = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
     log("decode: building layers")
     dec = bench_decode(args, opts)
-    log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s (kernel {dec['achieved']:.0f} GB/s)")
+    kern = dec["kern"]
+    k_us = sum(v["us"] for v in kern.values())
+    achieved = dec["step_bytes"] / (k_us * 1e-6) / 1e9
+    log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s; kernel launches "
+        f"{k_us:.1f} us/layer -> {achieved:.0f} GB/s")
+    traffic = load_traffic(kern)
     pre = None
     if not args.no_prefill:
         log("prefill: M=2048")
@@ -299,11 +340,16 @@ def main():
         "config": {"workload": "decode M=1, Llama-3-8B-shaped layer (q,k,v,o,gate,up,down), 4-bit NF4 + double "
                                "quant, group 128, outlier_frac 0.001 (BASELINE config 3); 10 rotating copies",
                    "M": 1, "bytes_per_step": dec["step_bytes"], "frac_of_hbm_peak": round(dec["value"] / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(dec["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "ts::decode_kernel<4,128,bf16>, 7 launches per step (one layer); achieved = "
-                               "step bytes / mean step GPU time from events around each graph replay",
-                     "step_gpu_us": round(dec["step_gpu_us"], 2), "per_linear": dec["detail"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["bytes_per_step"] if traffic else None,
+                     "kernel": "ts::decode_kernel (4-bit NF4 + DQ, group 128, bf16), one launch per linear; "
+                               "achieved = algorithmic bytes of the 7 launches of a layer / sum of their "
+                               "average launch durations (HIP events around graph replays of each linear "
+                               "over the 10 copies); traffic = HBM bytes of those 7 launches (PMC)",
+                     "launch_us_per_layer": round(k_us, 2), "step_gpu_us": round(dec["step_gpu_us"], 2),
+                     "per_linear": kern,
+                     "traffic_per_linear": traffic["per_linear_bytes"] if traffic else None},
         "prefill": pre,
         "cpu_baseline": cpu,
     }
