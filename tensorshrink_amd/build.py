@@ -35,6 +35,18 @@ SOURCES = [
     "ts_decode_b8_g64.hip",
     "ts_decode_b8_g128.hip",
     "ts_prefill.hip",
+    "ts_prefill_b2_g64.hip",
+    "ts_prefill_b2_g128.hip",
+    "ts_prefill_b2_g256.hip",
+    "ts_prefill_b4_g32.hip",
+    "ts_prefill_b4_g64.hip",
+    "ts_prefill_b4_g128.hip",
+    "ts_prefill_b4_g256.hip",
+    "ts_prefill_b6_g64.hip",
+    "ts_prefill_b6_g128.hip",
+    "ts_prefill_b8_g32.hip",
+    "ts_prefill_b8_g64.hip",
+    "ts_prefill_b8_g128.hip",
     "ts_aux.hip",
     "ts_quantize.hip",
 ]

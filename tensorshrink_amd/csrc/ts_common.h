@@ -70,6 +70,22 @@ TS_DEV ts_u32x4 ts_ld16(const void* p) { return *reinterpret_cast<const ts_u32x4
 TS_DEV ts_u32x2 ts_ld8(const void* p) { return *reinterpret_cast<const ts_u32x2*>(p); }
 TS_DEV uint32_t ts_ld4(const void* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
+// Raw buffer resource over `bytes` bytes at `base` (stride 0, gfx9 dword 3).
+// Loads through it take a 32-bit byte offset in one VGPR (the 64-bit base
+// stays in SGPRs) and return zero at offsets past `bytes` instead of faulting.
+TS_DEV __amdgpu_buffer_rsrc_t ts_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+TS_DEV ts_u32x4 ts_bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(ts_u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+TS_DEV ts_u32x2 ts_bld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(ts_u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+TS_DEV uint32_t ts_bld4(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
+TS_DEV uint32_t ts_bld2(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0); }
+TS_DEV uint32_t ts_bld1(__amdgpu_buffer_rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0); }
+
 // Kernel-argument pinning. The compiler treats kernel arguments as invariant
 // loads and re-fetches them lazily, in dependent batches of scalar loads (each
 // a memory round trip) wherever SGPR pressure is high. Passing a value
