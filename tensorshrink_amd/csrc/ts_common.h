@@ -79,6 +79,10 @@ TS_DEV __amdgpu_buffer_rsrc_t ts_rsrc(const void* base, uint32_t bytes) {
 TS_DEV ts_u32x4 ts_bld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(ts_u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+// Same, with a wave-uniform byte offset `soff` added in the scalar offset field.
+TS_DEV ts_u32x4 ts_bld16s(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff) {
+  return __builtin_bit_cast(ts_u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, 0));
+}
 TS_DEV ts_u32x2 ts_bld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(ts_u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }

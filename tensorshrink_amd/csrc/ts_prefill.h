@@ -8,20 +8,25 @@
 // that tile's outliers in (w = cast(f32(w) + delta), as modules.py:918 does on
 // the dense W) and feeds MFMA f32_32x32x16 with fp32 accumulation.
 //
-// Tile: 256 x BN x 64 per workgroup of 4 waves (2 x 2), each wave 128 x BN/2
-// as 4 x BN/64 MFMA 32x32 blocks; one wave per SIMD.
-//   * Raw global loads (x chunks, packed codes, scale / double-quant metadata)
-//     go into two register stages and are issued two k-steps ahead, all
-//     unconditional (addresses clamped into valid memory), so the compiler's
-//     wait counts stay exact and a k-step only waits for the stage it
-//     dequantizes. Nothing computes on loaded data in the load phase.
-//   * Each k-step runs 4 MFMA sub-steps on LDS buffer `cur`, each followed by
-//     a quarter of the next k-step's dequant (and x copy) into buffer
-//     `cur ^ 1`, so the VALU work overlaps the matrix core; one LDS-only
-//     barrier per k-step (a __syncthreads would drain the prefetch).
+// Tile: 256 x BN x 64 per workgroup of NW waves (NW/2 along M, 2 along N),
+// each wave (512/NW) x BN/2 as MFMA 32x32 blocks. NW = 8 (two waves per
+// SIMD, so one wave's LDS and barrier waits overlap the other's MFMAs) is
+// the default; NW = 4 gives one wave per SIMD with 128 x BN/2 wave tiles.
+//   * All global reads are raw buffer loads (64-bit bases in SGPRs, 32-bit
+//     offsets) into register stages: weights two k-steps ahead, x (two
+//     register sets) two k-steps ahead. Nothing computes on loaded data in the
+//     load phase and no load is conditional, so the compiler's wait counts
+//     stay exact and a wait never drains younger loads.
+//   * Each k-step runs 4 MFMA sub-steps on LDS buffer `cur`. The operand
+//     fragments and codebook values of sub-step s + 1 are read from LDS before
+//     sub-step s's MFMAs; the next k-step's dequant (scale, convert, write to
+//     buffer `cur ^ 1`) is spread over the sub-steps. One LDS-only barrier
+//     per k-step (a __syncthreads would drain the prefetch).
 //   * LDS tiles use a 16-byte-chunk XOR swizzle (chunk c of row r at
 //     c ^ (r & 7)): both the tile writes and the MFMA operand reads are
 //     bank-conflict free.
+//   * Codebooks sit in LDS as 32 bank-interleaved copies, one per lane of a
+//     half-wave, so random code lookups are conflict free.
 //   * Outliers: each tile row's outliers (up to OMAX) are staged in LDS
 //     sorted by column at the start; the threads owning the row walk them
 //     with a moving pointer. Outliers of a row beyond OMAX (none at the
@@ -68,7 +73,10 @@ struct PrefillArgs {
 
 constexpr int PF_BM = 256;
 constexpr int PF_BK = 64;
-constexpr int PF_OMAX = 64;  // outliers per tile row staged in LDS
+constexpr int PF_OMAX = 32;  // outliers per tile row staged in LDS
+#ifndef PF_NW
+#define PF_NW 8  // waves per workgroup
+#endif
 
 typedef __bf16 ts_bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 ts_f16x2 __attribute__((ext_vector_type(2)));
@@ -86,12 +94,14 @@ TS_DEV uint32_t to_pair(float lo, float hi) {
 // LDS offset (in uint16 elements) of 16-byte chunk c of row r in a [rows][64] tile.
 TS_DEV int swz(int r, int c) { return r * PF_BK + ((c ^ (r & 7)) << 3); }
 
-template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN>
-__global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in) {
+template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN, int NW>
+__global__ __launch_bounds__(64 * NW, NW / 4) void prefill_kernel(const PrefillArgs a_in) {
   constexpr int BM = PF_BM, BK = PF_BK;
-  constexpr int TM = BM / 64, TN = BN / 64;
-  constexpr int A_CHUNKS = BM * 8 / 256;      // 16-byte x chunks per thread per k-step
-  constexpr int CPT = BN * BK / 256;          // weight codes per thread per k-step
+  constexpr int NT = 64 * NW;                  // threads
+  constexpr int WGM = NW / 2;                  // waves along M (two along N)
+  constexpr int TM = BM / WGM / 32, TN = BN / 64;
+  constexpr int A_CHUNKS = BM * 8 / NT;       // 16-byte x chunks per thread per k-step
+  constexpr int CPT = BN * BK / NT;           // weight codes per thread per k-step
   constexpr int TPR = BK / CPT;               // threads per weight row
   constexpr int WB = CPT * BITS / 8;          // packed bytes per thread per k-step
   constexpr int WB2 = RVQ ? CPT / 4 : 0;      // RVQ stage-2 bytes
@@ -101,6 +111,11 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
   static_assert(C8 % 4 == 0 || C8 == 2, "dequant chunks per sub-step");
   static_assert(WB % 4 == 0, "packed chunk");
   extern __shared__ __align__(16) unsigned char smem[];
+  // The codebook is static LDS (its address folds into the ds_read offset),
+  // in 32 copies interleaved entry-major: copy l of entry e at [e * 32 + l],
+  // i.e. in bank l. Lane l reads copy l % 32, so a wave's 64 random lookups
+  // are bank-conflict free (two passes) whatever the codes.
+  __shared__ float cbs[CB ? CBN * 32 : 1];
 
   // Kernel arguments fetched once, kept in SGPRs (see the decode kernel).
   PrefillArgs a = a_in;
@@ -117,12 +132,12 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
 
   uint16_t* As = reinterpret_cast<uint16_t*>(smem);             // [2][BM][64]
   uint16_t* Bs = As + 2 * BM * BK;                              // [2][BN][64]
-  float* cbs = reinterpret_cast<float*>(Bs + 2 * BN * BK);      // codebook
-  uint32_t* ol = reinterpret_cast<uint32_t*>(cbs + CBN);        // [BN][OMAX] col | f16 delta << 16
+  uint32_t* ol = reinterpret_cast<uint32_t*>(Bs + 2 * BN * BK);  // [BN][OMAX] col | f16 delta << 16
   int32_t* ocnt = reinterpret_cast<int32_t*>(ol + BN * PF_OMAX);  // [BN] outliers per tile row
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const uint32_t cb_lane = lane & 31;  // codebook copy of this lane
+  const int wm = wave % WGM, wn = wave / WGM;
 
   // XCD-aware tile order: consecutive workgroups go to different XCDs, so map
   // blockIdx so that the workgroups sharing an XCD walk down one column of M
@@ -176,23 +191,28 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
   uint32_t xoff[A_CHUNKS];
 #pragma unroll
   for (int i = 0; i < A_CHUNKS; ++i) {
-    const int ch = tid + i * 256;
+    const int ch = tid + i * NT;
     xoff[i] = (uint32_t)(min(m0 + (ch >> 3), a.M - 1) * a.ldx) * 2u + (ch & 7) * 16u;
   }
+  // A chunk whose columns lie past `cols` (all eight: cols % 8 == 0) is read
+  // at an offset with bit 31 set, past the buffer's extent, which the buffer
+  // load returns as zeros.
+  const int xcol = (tid & 7) * 8;  // the same column slot for all of a thread's chunks
+  // The k-step's byte offset goes in the scalar offset; a lane whose columns
+  // are out of range ORs bit 31 into its vector offset, which is range checked.
   auto load_x = [&](int kt, ts_u32x4* xr) {
-    const uint32_t kb = (uint32_t)min(kt, KT - 1) * (BK * 2);
+    kt = min(kt, KT - 1);
+    const uint32_t kb = (uint32_t)kt * (BK * 2);
+    const uint32_t oob = (kt * BK + xcol < a.cols) ? 0u : 0x80000000u;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) xr[i] = ts_bld16(rx, xoff[i] + kb);
+    for (int i = 0; i < A_CHUNKS; ++i) xr[i] = ts_bld16s(rx, xoff[i] | oob, kb);
   };
-  auto store_x = [&](int buf, int kt, const ts_u32x4* xr) {
+  auto store_x = [&](int buf, const ts_u32x4* xr) {
     uint16_t* Ab = As + buf * BM * BK;
-    const int64_t k0 = (int64_t)kt * BK;
 #pragma unroll
     for (int i = 0; i < A_CHUNKS; ++i) {
-      const int ch = tid + i * 256;
-      const int r = ch >> 3, c = ch & 7;
-      const bool inb = k0 + c * 8 < a.cols;
-      *reinterpret_cast<ts_u32x4*>(Ab + swz(r, c)) = inb ? xr[i] : ts_u32x4{0u, 0u, 0u, 0u};
+      const int ch = tid + i * NT;
+      *reinterpret_cast<ts_u32x4*>(Ab + swz(ch >> 3, ch & 7)) = xr[i];
     }
   };
   auto load_stage = [&](int kt, Stage& S) {
@@ -239,40 +259,28 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
   };
 
   // ---- dequant of one stage into LDS, in 4 parts (one per MFMA sub-step) ---
-  // Moving pointer over this row's sorted outliers.
-  int opos = 0;
-  int oncnt = 0;  // staged outliers of this row (set after staging)
-  int64_t o_begin = 0, o_count = 0;
-  auto dequant_part = [&](const Stage& S, int part, int buf, int kt) {
-    uint16_t* Bb = Bs + buf * BN * BK;
-    const int k0 = kt * BK;
-    constexpr int CP = C8 >= 4 ? C8 / 4 : 1;  // 8-code chunks per part
+  // Split in two so the code-value fetch (codebook reads from LDS) of part
+  // p + 1 is in flight while part p's MFMAs run: lookup() gives the float code
+  // values of the part's chunks, finish() scales, converts and writes them.
+  constexpr int CP = C8 >= 4 ? C8 / 4 : 1;  // 8-code chunks per part
+  struct Codes {
+    float v[CP][8];
+  };
+  auto chunk_of = [&](int part, int cc) { return (C8 >= 4 ? part * CP : part) + cc; };
+  auto lookup = [&](const Stage& S, int part, Codes& C) {
     if (C8 < 4 && part >= C8) return;
 #pragma unroll
     for (int cc = 0; cc < CP; ++cc) {
-      const int c8 = (C8 >= 4 ? part * CP : part) + cc;
-      const int t = (c8 * 8) / (CPT >= GS ? GS : CPT);  // group of this chunk within the thread's codes
-      const int tg = NGT > 1 ? t : 0;
-      float s, gm;
-      if constexpr (DQ) {  // modules.py:573-579: code * meta_scale + meta_min in float32
-        s = __fadd_rn(__fmul_rn((float)S.sc[tg], ts_h2f(S.sm[tg] & 0xffffu)), ts_h2f(S.sm[tg] >> 16));
-        gm = __fadd_rn(__fmul_rn((float)S.gc[tg], ts_h2f(S.gm[tg] & 0xffffu)), ts_h2f(S.gm[tg] >> 16));
-      } else {
-        s = ts_h2f((uint16_t)S.sc[tg]);
-        gm = ts_h2f((uint16_t)S.gc[tg]);
-      }
-      float cv[8];
+      const int c8 = chunk_of(part, cc);
+      float* cv = C.v[cc];
       if constexpr (BITS == 4) {
         const uint32_t d = S.w[c8];
         if constexpr (CB) {
-          const uint32_t lo = (d << 2) & 0x3c3c3c3cu, hi = (d >> 2) & 0x3c3c3c3cu;  // 4*code per byte
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            cv[2 * e] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cbs) + ((lo >> (8 * e)) & 0xffu));
-            cv[2 * e + 1] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(cbs) + ((hi >> (8 * e)) & 0xffu));
-          }
+          for (int e = 0; e < 8; ++e) cv[e] = cbs[(((d >> (4 * e)) & 15u) << 5) | cb_lane];
         } else {
-          const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+          uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+          asm volatile("" : "+v"(lo), "+v"(hi));  // keeps the byte-select conversions (v_cvt_f32_ubyteN)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             cv[2 * e] = (float)((lo >> (8 * e)) & 0xffu);
@@ -284,7 +292,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const uint32_t c = (d >> (2 * e)) & 3u;
-          cv[e] = CB ? cbs[c] : (float)c;
+          cv[e] = CB ? cbs[(c << 5) | cb_lane] : (float)c;
         }
       } else {
 #pragma unroll
@@ -293,10 +301,39 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const uint32_t c = (d >> (8 * e)) & 0xffu;
-            cv[4 * h + e] = CB ? cbs[c] : (float)c;
+            cv[4 * h + e] = CB ? cbs[(c << 5) | cb_lane] : (float)c;
           }
         }
       }
+    }
+  };
+  // Per-group scale and offset of a stage (float32, modules.py:573-579 for
+  // the double-quant codes), computed once per k-step.
+  struct Scales {
+    float s[NGT], g[NGT];
+  };
+  auto scales = [&](const Stage& S, Scales& Q) {
+#pragma unroll
+    for (int t = 0; t < NGT; ++t) {
+      if constexpr (DQ) {  // code * meta_scale + meta_min
+        Q.s[t] = __fadd_rn(__fmul_rn((float)S.sc[t], ts_h2f(S.sm[t] & 0xffffu)), ts_h2f(S.sm[t] >> 16));
+        Q.g[t] = __fadd_rn(__fmul_rn((float)S.gc[t], ts_h2f(S.gm[t] & 0xffffu)), ts_h2f(S.gm[t] >> 16));
+      } else {
+        Q.s[t] = ts_h2f((uint16_t)S.sc[t]);
+        Q.g[t] = ts_h2f((uint16_t)S.gc[t]);
+      }
+    }
+  };
+  auto finish = [&](const Stage& S, const Scales& Q, int part, int buf, const Codes& C) {
+    if (C8 < 4 && part >= C8) return;
+    uint16_t* Bb = Bs + buf * BN * BK;
+#pragma unroll
+    for (int cc = 0; cc < CP; ++cc) {
+      const int c8 = chunk_of(part, cc);
+      const int t = (c8 * 8) / (CPT >= GS ? GS : CPT);  // group of this chunk within the thread's codes
+      const int tg = NGT > 1 ? t : 0;
+      const float s = Q.s[tg], gm = Q.g[tg];
+      const float* cv = C.v[cc];
       float v[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(cv[e], s, gm);
@@ -314,8 +351,17 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
       const int chunk = (wpart * CPT) / 8 + c8;
       *reinterpret_cast<ts_u32x4*>(Bb + swz(wr, chunk)) = pk;
     }
-    if (part == 3 && o_count > 0) {
-      // fold this row's outliers that land in the thread's slice of the k-step
+  };
+  // Moving pointer over this row's sorted outliers.
+  int opos = 0;
+  int oncnt = 0;  // staged outliers of this row (set after staging)
+  int64_t o_begin = 0, o_count = 0;
+  // Fold this row's outliers that land in the thread's slice of k-step kt
+  // into the dequantized tile (w = cast(f32(w) + delta), modules.py:918).
+  auto fold_outliers = [&](int buf, int kt) {
+    uint16_t* Bb = Bs + buf * BN * BK;
+    const int k0 = kt * BK;
+    if (o_count > 0) {
       const int kc0 = k0 + wpart * CPT, kc1 = kc0 + CPT;
       while (opos < oncnt) {
         const uint32_t e = ol[wr * PF_OMAX + opos];
@@ -338,7 +384,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
   load_x(1, X1);
   load_stage(1, S1);
   if constexpr (CB) {
-    for (int i = tid; i < CBN; i += 256) cbs[i] = a.codebook[i];
+    for (int i = tid; i < CBN * 32; i += NT) cbs[i] = a.codebook[i >> 5];
   }
   // stage each tile row's first OMAX outliers, sorted by column (K < 65536)
   {
@@ -364,8 +410,15 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
   ts_lds_barrier();
   oncnt = ocnt[wr];
 #pragma unroll
-  for (int part = 0; part < 4; ++part) dequant_part(S0, part, 0, 0);
-  store_x(0, 0, X0);
+  for (int part = 0; part < 4; ++part) {
+    Codes C;
+    Scales Q;
+    scales(S0, Q);
+    lookup(S0, part, C);
+    finish(S0, Q, part, 0, C);
+  }
+  fold_outliers(0, 0);
+  store_x(0, X0);
   load_stage(2, S0);
   ts_lds_barrier();
 
@@ -375,38 +428,65 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = ts_f32x16{};
 
-  // One k-step: x for k-step kt + 2 is issued into XL first; MFMAs on LDS
-  // buffer `cur`, interleaved with the dequant of stage S (k-step kt + 1)
-  // into the other buffer; S is refilled with k-step kt + 3; then x for
-  // k-step kt + 1 (issued a k-step ago, in XS) goes to the other buffer.
-  auto kstep = [&](int kt, Stage& S, ts_u32x4* XL, const ts_u32x4* XS) {
-    const int cur = kt & 1;
+  // MFMA operand fragments of one 16-wide k slice (sub-step s of a k-step).
+  struct Frag {
+    ts_u32x4 a[TM], b[TN];
+  };
+  auto read_frag = [&](int cur, int s, Frag& F) {
     const uint16_t* Ab = As + cur * BM * BK;
     const uint16_t* Bb = Bs + cur * BN * BK;
+    const int c = 2 * s + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) F.a[i] = *reinterpret_cast<const ts_u32x4*>(Ab + swz(wm * (BM / WGM) + 32 * i + (lane & 31), c));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) F.b[j] = *reinterpret_cast<const ts_u32x4*>(Bb + swz(wn * (BN / 2) + 32 * j + (lane & 31), c));
+  };
+  auto mfma = [&](const Frag& F) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = ts_mfma32x32x16<BF16>(F.a[i], F.b[j], acc[i][j]);
+  };
+
+  // One k-step. The LDS reads (operand fragments, code values) of sub-step
+  // s + 1 are issued before sub-step s's MFMAs, whose shadow then covers
+  // their latency and the VALU work of finish(). x for k-step kt + 2 is
+  // issued into XL at the start; the dequant of stage S (k-step kt + 1) goes
+  // to the other LDS buffer; S is refilled with k-step kt + 3; then x for
+  // k-step kt + 1 (issued a k-step ago, in XS) is stored to the other buffer.
+  auto kstep = [&](int kt, Stage& S, ts_u32x4* XL, const ts_u32x4* XS) {
+    const int cur = kt & 1, nxt = cur ^ 1;
+    Frag F0, F1;
+    Codes C0, C1;
+    Scales Q;
+    read_frag(cur, 0, F0);
+    lookup(S, 0, C0);
+    scales(S, Q);
     load_x(kt + 2, XL);
-    asm volatile("" ::: "memory");  // keep the x loads here, ahead of the MFMA phase
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      const int c = 2 * s + (lane >> 5);
-      ts_u32x4 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * (BM / 2) + 32 * i + (lane & 31);
-        af[i] = *reinterpret_cast<const ts_u32x4*>(Ab + swz(r, c));
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * (BN / 2) + 32 * j + (lane & 31);
-        bf[j] = *reinterpret_cast<const ts_u32x4*>(Bb + swz(r, c));
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = ts_mfma32x32x16<BF16>(af[i], bf[j], acc[i][j]);
-      dequant_part(S, s, cur ^ 1, kt + 1);
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    read_frag(cur, 1, F1);
+    lookup(S, 1, C1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(F0);
+    finish(S, Q, 0, nxt, C0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frag(cur, 2, F0);
+    lookup(S, 2, C0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(F1);
+    finish(S, Q, 1, nxt, C1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frag(cur, 3, F1);
+    lookup(S, 3, C1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(F0);
+    finish(S, Q, 2, nxt, C0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma(F1);
+    finish(S, Q, 3, nxt, C1);
+    fold_outliers(nxt, kt + 1);
     load_stage(kt + 3, S);
-    store_x(cur ^ 1, kt + 1, XS);
+    store_x(nxt, XS);
     ts_lds_barrier();
   };
   // two k-steps per iteration (stages and x sets alternate), one exit
@@ -430,7 +510,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
       for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int64_t m = min(m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), a.M - 1);
+          const int64_t m = min(m0 + wm * (BM / WGM) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), a.M - 1);
           acc[i][j][r] += XT<BF16>::to_f((uint16_t)ts_bld2(rx, ((uint32_t)(m * a.ldx) + col) * 2u)) * d;
         }
       }
@@ -440,7 +520,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int64_t m = m0 + wm * (BM / WGM) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m >= a.M) continue;
         const float v = acc[i][j][r] + b;
         const int64_t off = m * a.ldy + n;
@@ -454,34 +534,34 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
 template <int BITS, bool CB, int BN>
 inline size_t prefill_smem() {
   constexpr int CBN = (CB && BITS == 8) ? 256 : 16;
-  return (size_t)2 * (PF_BM + BN) * PF_BK * 2 + CBN * 4 + (size_t)BN * PF_OMAX * 4 + (size_t)BN * 4;
+  (void)CBN;  // the codebook is static LDS
+  return (size_t)2 * (PF_BM + BN) * PF_BK * 2 + (size_t)BN * PF_OMAX * 4 + (size_t)BN * 4;
 }
 
-template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN>
+template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN, int NW>
 inline int launch_prefill(PrefillArgs a, hipStream_t st) {
   const size_t smem = prefill_smem<BITS, CB, BN>();
-  auto kern = prefill_kernel<BITS, GS, BF16, CB, RVQ, DQ, BN>;
+  auto kern = prefill_kernel<BITS, GS, BF16, CB, RVQ, DQ, BN, NW>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess)
+                            (int)smem) != hipSuccess)
       return TS_HIP_ERROR;
     attr_set = true;
   }
   a.m_tiles = ts_cdiv(a.M, PF_BM);
   a.n_tiles = ts_cdiv(a.N, BN);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(a.m_tiles * a.n_tiles)), dim3(256), smem, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(a.m_tiles * a.n_tiles)), dim3(64 * NW), smem, st, a);
   TS_CHECK_LAUNCH();
   return TS_OK;
 }
 
-// 256 x 128 tiles: with two k-steps of weights in flight in registers a
-// 256 x 256 tile does not fit the 256 architectural VGPRs of a wave (the
-// accumulators take all 256 AGPRs) and spills.
+// 256 x 128 tiles: a 256 x 256 tile with two k-steps of loads in flight does
+// not fit the registers of a wave (its accumulators alone take 256).
 template <int BITS, int GS, bool BF16, bool CB, bool RVQ>
 inline int launch_prefill_tiles(PrefillArgs& a, hipStream_t st) {
-  if (a.dqsc != nullptr) return launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128>(a, st);
-  return launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128>(a, st);
+  if (a.dqsc != nullptr) return launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, PF_NW>(a, st);
+  return launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128, PF_NW>(a, st);
 }
 
 // Per-(bit width, group size) launchers, one translation unit each

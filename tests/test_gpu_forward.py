@@ -109,6 +109,20 @@ def test_cfg3_llama8b_layer():
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("bits,frac", [(4, 0.05), (8, 0.03), (6, 0.02)])
+def test_forward_dense_outliers(bits, frac):
+    """Rows with more outliers than the prefill kernel stages per tile row
+    (their rest is added in the epilogue) and more than the decode kernel's
+    default slot count."""
+    opts = dict(bits=bits, group_size=128, outlier_frac=frac, double_quant=True, nf_quant=bits != 6)
+    ql, W = _layer(256, 2048, 31 + bits, opts)
+    for M in (1, 16, 64, 300):
+        x = recipes.activations(M, 2048, seed=M).cuda()
+        err = max_rel_err(ql(x).float(), x.float() @ W.T)
+        say("dense outliers", bits, frac, M, err)
+        assert err <= TOL, (M, err)
+
+
 @pytest.mark.slow
 @pytest.mark.parametrize("bits", [8, 6])
 def test_cfg4_prefill_2048(bits):
