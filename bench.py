@@ -8,14 +8,17 @@ Workload (`value`): decode at M=1 through the seven linears of a
 Llama-3-8B-shaped decoder layer (q 4096x4096, k/v 1024x4096, o 4096x4096,
 gate/up 14336x4096, down 4096x14336), 4-bit NF4 + double quant, group 128,
 0.1 % outliers (the 4-bit M=1 decode target). One step is
-one layer forward (7 QuantLinear calls, one kernel launch each). Ten copies of
-the layer (1.2 GB) are rotated so every step streams its weights from HBM and
-not from the 256 MB MALL; each copy's step is a captured HIP graph.
+one layer forward: the seven QuantLinear forwards in four launches, q/k/v and
+gate/up each one grouped launch over layers that share their input
+(QuantLinear.forward_group), o and down one launch each (--ungrouped: seven
+launches). Ten copies of the layer (1.2 GB) are rotated so every step streams
+its weights from HBM and not from the 256 MB MALL; each copy's step is a
+captured HIP graph.
 
 Alongside it (extra keys of the same JSON line):
-  * "roofline"     - the decode kernel: algorithmic bytes of every launch in the
-                     timed region / their summed durations (HIP events around
-                     each launch, recorded inside the graphs), vs 8 TB/s;
+  * "roofline"     - the decode kernel: algorithmic bytes of a step's launches /
+                     the sum of their average durations (HIP events around
+                     graph replays of each launch over the copies), vs 8 TB/s;
   * "prefill"      - BASELINE config 4: gate/up/down at M=2048, 8-bit NF8 + DQ
                      and 6-bit RVQ, 2*M*N*K flops / kernel time vs 2.5 PFLOP/s;
   * "cpu_baseline" - the reference CPU fallback forward (bf16 dequant + F.linear,
@@ -89,6 +92,21 @@ def build_decode_layer(opts):
     return layer
 
 
+# Launches of one decode step: (name, positions in LLAMA3_8B_LINEARS).
+GROUPED_UNITS = [("qkv", (0, 1, 2)), ("o", (3,)), ("gate_up", (4, 5)), ("down", (6,))]
+SINGLE_UNITS = [(n, (i,)) for i, n in enumerate(("q", "k", "v", "o", "gate", "up", "down"))]
+
+
+def run_unit(layer, idx, xs):
+    """The forwards of one launch unit (a list of outputs)."""
+    import tensorshrink_amd as ts
+    qs = [layer[i][1] for i in idx]
+    x = xs[qs[0].in_features]
+    if len(qs) == 1:
+        return [qs[0](x)]
+    return ts.QuantLinear.forward_group(qs, x)
+
+
 def bench_decode(args, opts):
     import recipes
     torch.cuda.synchronize()
@@ -96,17 +114,18 @@ def bench_decode(args, opts):
     copies = [base] + [[(n, clone_layer(q)) for n, q in base] for _ in range(args.copies - 1)]
     xs = {4096: recipes.activations(1, 4096).cuda(), 14336: recipes.activations(1, 14336).cuda()}
     step_bytes = sum(layer_bytes(q, 1) for _, q in base)
+    units = SINGLE_UNITS if args.ungrouped else GROUPED_UNITS
     stream = torch.cuda.Stream()
     graphs, outs = [], []
     with torch.cuda.stream(stream):
         for layer in copies:  # warm every kernel instantiation outside capture
-            for _, q in layer:
-                q(xs[q.in_features])
+            for _, idx in units:
+                run_unit(layer, idx, xs)
         torch.cuda.synchronize()
         for layer in copies:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
-                outs.append([q(xs[q.in_features]) for _, q in layer])
+                outs.append([run_unit(layer, idx, xs) for _, idx in units])
             graphs.append(g)
         torch.cuda.synchronize()
         for s in range(args.warmup):
@@ -128,58 +147,61 @@ def bench_decode(args, opts):
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     gpu_ms = [a.elapsed_time(b) for a, b in evs[1:]]  # the first pair starts on an idle queue
     step_gpu_ms = sum(gpu_ms) / len(gpu_ms)
-    kern = per_linear_kernel_time(copies, xs, stream, reps=args.kernel_reps)
+    kern = unit_kernel_time(copies, xs, stream, units, reps=args.kernel_reps)
     return dict(ms_per_step=ms_per_step, value=value, step_bytes=step_bytes, kern=kern,
-                base=base, xs=xs, step_gpu_us=step_gpu_ms * 1e3)
+                base=base, xs=xs, step_gpu_us=step_gpu_ms * 1e3, units=units)
 
 
-def per_linear_kernel_time(copies, xs, stream, reps: int):
-    """Average decode-kernel launch duration per linear: one graph per linear
-    position holding that linear's launch on every copy (back to back, the
-    weights rotating so none comes from the MALL), replayed `reps` times
-    between two HIP events on the launch stream. The per-launch average
-    includes the dispatch gap between consecutive kernels of a graph."""
+def unit_kernel_time(copies, xs, stream, units, reps: int):
+    """Average decode launch duration per launch unit: one graph per unit
+    holding that unit's launch on every copy (back to back, the weights
+    rotating so none comes from the MALL), replayed `reps` times between two
+    HIP events on the launch stream. The per-launch average includes the
+    dispatch gap between consecutive kernels of a graph."""
     out = {}
     with torch.cuda.stream(stream):
         graphs = []
-        for p, (name, q0) in enumerate(copies[0]):
+        for name, idx in units:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
                 for layer in copies:
-                    layer[p][1](xs[q0.in_features])
-            graphs.append((name, q0, g))
+                    run_unit(layer, idx, xs)
+            graphs.append((name, idx, g))
         for _, _, g in graphs:
             g.replay()
         torch.cuda.synchronize()
         evs = []
-        for name, q0, g in graphs:
+        for name, idx, g in graphs:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
             for _ in range(reps):
                 g.replay()
             e1.record(stream)
-            evs.append((name, q0, e0, e1))
+            evs.append((name, idx, e0, e1))
         torch.cuda.synchronize()
-    for name, q0, e0, e1 in evs:
+    for name, idx, e0, e1 in evs:
         us = e0.elapsed_time(e1) * 1e3 / (reps * len(copies))
-        nb = layer_bytes(q0, 1)
-        out[name] = {"shape": [q0.out_features, q0.in_features], "bytes": nb, "us": round(us, 2),
+        qs = [copies[0][i][1] for i in idx]
+        nb = sum(layer_bytes(q, 1) for q in qs)
+        out[name] = {"shapes": [[q.out_features, q.in_features] for q in qs], "bytes": nb, "us": round(us, 2),
                      "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
     return out
 
 
-def load_traffic(detail):
+def load_traffic(units):
     """HBM bytes per launch from the committed PMC summary (FETCH_SIZE and
     WRITE_SIZE passes of rocprofv3 over this bench, each scaled by the same
-    counter's reading for a plain copy of known size), or None."""
+    counter's reading for a plain copy of known size), or None. A grouped
+    launch is the sum of its layers' launches."""
     path = os.path.join(ROOT, "profiles", "decode_traffic.json")
     if not os.path.exists(path):
         return None
+    names = ("q", "k", "v", "o", "gate", "up", "down")
     try:
         t = json.load(open(path))
         per = t["per_linear_bytes"]
-        return {"bytes_per_step": int(sum(per[n] for n in detail)),
-                "per_linear_bytes": {n: int(per[n]) for n in detail},
+        pu = {u: int(sum(per[names[i]] for i in idx)) for u, idx in units}
+        return {"bytes_per_step": int(sum(pu.values())), "per_launch_bytes": pu,
                 "source": "profiles/decode_traffic.json"}
     except (OSError, KeyError, ValueError):
         return None
@@ -294,6 +316,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
+    ap.add_argument("--ungrouped", action="store_true", help="one launch per linear (7 per step)")
     ap.add_argument("--copy-calib", action="store_true", help="only run the plain-copy PMC calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -313,7 +336,7 @@ def main():
     achieved = dec["step_bytes"] / (k_us * 1e-6) / 1e9
     log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s; kernel launches "
         f"{k_us:.1f} us/layer -> {achieved:.0f} GB/s")
-    traffic = load_traffic(kern)
+    traffic = load_traffic(dec["units"])
     pre = None
     if not args.no_prefill:
         log("prefill: M=2048")
@@ -338,18 +361,20 @@ def main():
         "dtype": "bf16 activations x 4-bit codes, fp32 accumulate",
         "data": "synthetic: seeded N(0,0.02) fp16 weights with 0.1% x20 outliers, N(0,1) bf16 activations",
         "config": {"workload": "decode M=1, Llama-3-8B-shaped layer (q,k,v,o,gate,up,down), 4-bit NF4 + double "
-                               "quant, group 128, outlier_frac 0.001 (BASELINE config 3); 10 rotating copies",
+                               "quant, group 128, outlier_frac 0.001 (BASELINE config 3); 10 rotating copies; "
+                               + ("7 launches per step" if args.ungrouped else
+                                  "4 launches per step (q/k/v and gate/up grouped)"),
                    "M": 1, "bytes_per_step": dec["step_bytes"], "frac_of_hbm_peak": round(dec["value"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic["bytes_per_step"] if traffic else None,
-                     "kernel": "ts::decode_kernel (4-bit NF4 + DQ, group 128, bf16), one launch per linear; "
-                               "achieved = algorithmic bytes of the 7 launches of a layer / sum of their "
-                               "average launch durations (HIP events around graph replays of each linear "
-                               "over the 10 copies); traffic = HBM bytes of those 7 launches (PMC)",
+                     "kernel": "ts::decode_kernel (4-bit NF4 + DQ, group 128, bf16); achieved = algorithmic "
+                               "bytes of a step's launches / sum of their average launch durations (HIP events "
+                               "around graph replays of each launch over the 10 copies); traffic = HBM bytes "
+                               "of those launches (PMC)",
                      "launch_us_per_layer": round(k_us, 2), "step_gpu_us": round(dec["step_gpu_us"], 2),
-                     "per_linear": kern,
-                     "traffic_per_linear": traffic["per_linear_bytes"] if traffic else None},
+                     "per_launch": kern,
+                     "traffic_per_launch": traffic["per_launch_bytes"] if traffic else None},
         "prefill": pre,
         "cpu_baseline": cpu,
     }

@@ -76,6 +76,11 @@ typedef struct {
    * NULL / 0 when the layer has no outliers. */
   const uint64_t* tile_outliers;
   int64_t tile_outlier_cap;
+  /* Optional host copy of `codebook` (no counterpart in the reference). With
+   * at most 16 entries the decode kernel then takes the values as launch
+   * arguments instead of reading them from device memory, where that read
+   * would queue behind the layer's weight stream. NULL: read `codebook`. */
+  const float* codebook_host;
 } ts_qlayer;
 
 const char* ts_status_str(int status);
@@ -98,6 +103,20 @@ size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M);
 int ts_qlinear_forward(const ts_qlayer* layer, const void* x, int64_t M, int64_t ldx, int x_dtype,
                        void* y, int64_t ldy, int y_dtype, const void* bias,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The forward above for n (1..4) layers that read the same x (q/k/v, gate/up)
+ * in one launch: y[l][M, rows_l] = x @ W_l^T (+ bias[l]). Covers M <= 16 with
+ * layers of one format (bits, group size, cols, codebook / double-quant /
+ * stage-2 kind); returns TS_NOT_COVERED otherwise, and the caller runs
+ * ts_qlinear_forward per layer. No counterpart in the reference, which calls
+ * fused_quantized_linear once per QuantLinear (modules.py:896-905); this
+ * replaces that sequence of calls for layers sharing an input. bias may be
+ * NULL, as may any bias[l].
+ */
+int ts_qlinear_forward_group(const ts_qlayer* const* layers, int n_layers, const void* x, int64_t M, int64_t ldx,
+                             int x_dtype, void* const* y, const int64_t* ldy, int y_dtype,
+                             const void* const* bias, void* stream);
 
 /*
  * out[m, row[k]] += x[m, col[k]] * delta[k] on an fp32 [M, ldo] buffer.

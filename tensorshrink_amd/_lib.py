@@ -38,7 +38,7 @@ class QLayer(ctypes.Structure):
         ("outlier_row", c_vp), ("outlier_col", c_vp), ("outlier_delta", c_vp), ("n_outliers", c_i64),
         ("outlier_row_ptr", c_vp),
         ("stage2_packed", c_vp), ("stage2_stride", c_i64), ("stage2_scale", c_vp), ("stage2_gmin", c_vp),
-        ("tile_outliers", c_vp), ("tile_outlier_cap", c_i64),
+        ("tile_outliers", c_vp), ("tile_outlier_cap", c_i64), ("codebook_host", c_vp),
     ]
 
 
@@ -60,6 +60,9 @@ PROTOTYPES = {
     "ts_forward_workspace_bytes": (c_sz, [ctypes.POINTER(QLayer), c_i64]),
     "ts_qlinear_forward": (ctypes.c_int, [ctypes.POINTER(QLayer), c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64,
                                           ctypes.c_int, c_vp, c_vp, c_sz, c_vp]),
+    "ts_qlinear_forward_group": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(QLayer)), ctypes.c_int, c_vp, c_i64,
+                                                c_i64, ctypes.c_int, ctypes.POINTER(c_vp), ctypes.POINTER(c_i64),
+                                                ctypes.c_int, ctypes.POINTER(c_vp), c_vp]),
     "ts_apply_outlier_correction": (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp,
                                                    c_i64, c_vp]),
     "ts_dequantize": (ctypes.c_int, [ctypes.POINTER(QLayer), ctypes.c_int, c_vp, c_vp, c_i64, c_vp, c_i64,

@@ -6,6 +6,9 @@
 namespace ts {
 int decode_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
                    int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st);
+int decode_forward_group(const ts_qlayer* const* layers, int n, const uint16_t* x, int64_t M, int64_t ldx,
+                         int x_dtype, void* const* y, const int64_t* ldy, int y_dtype,
+                         const uint16_t* const* bias, hipStream_t st);
 int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
                     int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st);
 int generic_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
@@ -100,6 +103,25 @@ int ts_qlinear_forward(const ts_qlayer* L, const void* x, int64_t M, int64_t ldx
   }
   if (rc == TS_NOT_COVERED) rc = ts::generic_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
   return rc;
+}
+
+int ts_qlinear_forward_group(const ts_qlayer* const* layers, int n_layers, const void* x, int64_t M, int64_t ldx,
+                             int x_dtype, void* const* y, const int64_t* ldy, int y_dtype,
+                             const void* const* bias, void* stream) {
+  if (!layers || !y || !ldy || !x || M < 0 || n_layers < 1) return TS_BAD_ARG;
+  if (x_dtype != TS_BF16 && x_dtype != TS_F16) return TS_BAD_ARG;
+  if (y_dtype != TS_BF16 && y_dtype != TS_F16 && y_dtype != TS_F32) return TS_BAD_ARG;
+  if (y_dtype != TS_F32 && y_dtype != x_dtype) return TS_BAD_ARG;
+  for (int l = 0; l < n_layers; ++l) {
+    const ts_qlayer* L = layers[l];
+    if (!layer_ok(L) || !y[l] || ldx < L->cols || ldy[l] < L->rows) return TS_BAD_ARG;
+  }
+  if (M == 0) return TS_OK;
+  const ts_qlayer* L0 = layers[0];
+  const bool aligned = (L0->cols % 8 == 0) && (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  if (!aligned || M > 16) return TS_NOT_COVERED;
+  return ts::decode_forward_group(layers, n_layers, static_cast<const uint16_t*>(x), M, ldx, x_dtype, y, ldy, y_dtype,
+                                  reinterpret_cast<const uint16_t* const*>(bias), S(stream));
 }
 
 int ts_apply_outlier_correction(float* out, int64_t M, int64_t ldo, const void* x, int64_t ldx, int x_dtype,

@@ -72,15 +72,29 @@ struct DecodeArgs {
   int64_t n_groups;
   int64_t n_tiles;
   int M;
-  const float* cbsrc;        // codebook, or any valid float array when cb_is_table == 0
-  int cb_is_table;
+  const float* cbsrc;        // codebook (read when cb_mode == CB_DEVICE)
+  int cb_mode;               // CB_UNIFORM, CB_INLINE (values in cbv) or CB_DEVICE
+  float cbv[16];             // the codebook with CB_INLINE
   const uint16_t* bias_src;  // bias, or any valid array when there is none
   int64_t bias_mul;          // 1 with a bias, else 0
 };
 
+// Several layers that read the same activations (q/k/v, gate/up) in one
+// launch: the grid is the concatenation of their tiles, and each workgroup
+// takes the arguments of the layer its tile belongs to.
+constexpr int DEC_GMAX = 4;  // layers per launch
+enum { CB_UNIFORM = 0, CB_INLINE = 1, CB_DEVICE = 2 };
+struct DecodeGroup {
+  DecodeArgs a[DEC_GMAX];
+  int64_t tile_end[DEC_GMAX];  // cumulative tile counts
+  int n;
+};
+
 constexpr size_t DEC_XLDS_MAX = 32 * 1024;  // activations staged in LDS up to this size
 enum { XM_GLOBAL = 0, XM_DMA = 1, XM_REG = 2 };
-constexpr int XREG_CHUNKS = 2;  // 16-byte x chunks per thread with XM_REG
+// 16-byte x chunks per thread with XM_REG: 4 with 8 waves (x up to 32 KB,
+// a 14336-wide row at M = 1), else 2.
+constexpr int xreg_chunks(int w) { return w == 8 ? 4 : 2; }
 
 template <bool BF16>
 TS_DEV uint32_t pack2(float lo, float hi) {
@@ -139,7 +153,7 @@ struct DecGeom {
 // longer runs through the two register buffers.
 // XM: where the A operand (x) comes from: XM_GLOBAL reads it from global
 // memory per MFMA (x too large for LDS); XM_REG stages it in LDS through
-// registers (at most XREG_CHUNKS 16-byte chunks per thread); XM_DMA stages it
+// registers (at most xreg_chunks(W) 16-byte chunks per thread); XM_DMA stages it
 // with direct global->LDS loads. XM_REG keeps the compiler's wait counts
 // exact, so a wave computes its first batch while the second is in flight;
 // with direct-to-LDS loads pending the compiler treats the load counter as
@@ -151,7 +165,7 @@ struct DecGeom {
 // of 16-row tiles are resident at once across 256 CUs.
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
           bool LOOP>
-__global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in) {
+__global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) {
   constexpr int NT = 64 * W;
   constexpr bool XLDS = XM != XM_GLOBAL;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -171,13 +185,18 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   // made opaque so the compiler keeps it in SGPRs. Otherwise it re-fetches
   // arguments lazily (they are invariant loads) in several dependent
   // batches, each a memory round trip on every workgroup's critical path.
-  DecodeArgs a = a_in;
+  const int64_t bid = blockIdx.x;
+  int li = 0;
+#pragma unroll
+  for (int i = 1; i < DEC_GMAX; ++i) li += (i < g.n && bid >= g.tile_end[i - 1]) ? 1 : 0;
+  DecodeArgs a = g.a[li];
+  const int64_t tile = bid - (li > 0 ? g.tile_end[li > 0 ? li - 1 : 0] : 0);
 #define TS_PG(f) ts_pin_global(a.f)
 #define TS_PS(f) ts_pin_scalar(a.f)
   TS_PG(packed); TS_PG(scale); TS_PG(gmin); TS_PG(dqsc); TS_PG(dqsm); TS_PG(dqgc); TS_PG(dqgm); TS_PG(x); TS_PG(y);
   TS_PG(slots); TS_PG(cbsrc); TS_PG(bias_src);
   TS_PS(pstride); TS_PS(dq_gs); TS_PS(ldx); TS_PS(ldy); TS_PS(N); TS_PS(cols); TS_PS(K); TS_PS(n_groups);
-  TS_PS(n_tiles); TS_PS(M); TS_PS(cb_is_table); TS_PS(cap); TS_PS(bias_mul); TS_PS(y_dtype);
+  TS_PS(n_tiles); TS_PS(M); TS_PS(cb_mode); TS_PS(cap); TS_PS(bias_mul); TS_PS(y_dtype);
   if constexpr (RVQ) { TS_PG(s2packed); TS_PS(s2stride); TS_PG(s2scale); TS_PG(s2gmin); }
 #undef TS_PG
 #undef TS_PS
@@ -408,7 +427,6 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   };
 
   // ---- one tile per workgroup, batches double-buffered ----------------------
-  const int64_t tile = blockIdx.x;
   if (tile >= a.n_tiles) return;
   const int64_t r0 = tile * 16;
   ts_f32x4 yacc = {0.f, 0.f, 0.f, 0.f};
@@ -422,7 +440,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   // clamped (valid) address; their bytes land in the padded tail of the
   // buffer or in the column padding, which is zeroed below. The issue loop is
   // unrolled to a compile-time bound with uniform predicates.
-  // XM_REG: XREG_CHUNKS 16-byte chunks per thread into registers, stored to
+  // XM_REG: XRC 16-byte chunks per thread into registers, stored to
   // LDS once every load of the tile is issued.
   // (32-bit arithmetic: with x staged, M * K * 2 <= DEC_XLDS_MAX.)
   const uint32_t kK = (uint32_t)a.K;
@@ -443,10 +461,11 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   }
   const uint32_t kch = kK / 8u;                                   // 16-byte chunks per x row
   const uint32_t xch8 = XM == XM_REG ? (uint32_t)a.M * kch : 1u;  // chunks of x
-  ts_u32x4 xr[XM == XM_REG ? XREG_CHUNKS : 1];
+  constexpr int XRC = xreg_chunks(W);
+  ts_u32x4 xr[XM == XM_REG ? XRC : 1];
   if constexpr (XM == XM_REG) {
 #pragma unroll
-    for (int i = 0; i < XREG_CHUNKS; ++i) {
+    for (int i = 0; i < XRC; ++i) {
       const uint32_t c = min((uint32_t)(tid + i * NT), xch8 - 1u);
       const uint32_t m = c / kch;
       const uint32_t k = min((c - m * kch) * 8u, (uint32_t)a.cols - 8u);
@@ -455,7 +474,12 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   }
   constexpr int NCB = 1 << (RVQ ? 4 : BITS);
   const int cbi = tid & 255;  // staged codebook slot (every writer of a slot writes the same value)
-  const float cbraw = a.cbsrc[(cbi < NCB && a.cb_is_table) ? cbi : 0];
+  // Codebook value of slot cbi. The device read is the only load behind a
+  // (uniform) branch: on the other paths no load is issued there, and the
+  // wait at its use then covers exactly the x loads issued before it, which
+  // that point needs anyway.
+  float cbv = (float)cbi;  // uniform grid
+  if (a.cb_mode == CB_DEVICE) cbv = a.cbsrc[cbi < NCB ? cbi : 0];
   Batch bufA, bufB;
   load_batch(tile, 0, bufA);
   load_batch(tile, 1, bufB);  // (a dead batch when nb == 1)
@@ -473,13 +497,19 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeArgs a_in
   // unconditional store (threads tid, tid + 256, ... write the same value to
   // slot tid % 256): a store under `tid < NCB` would let the compiler sink
   // the codebook load next to it and wait there for every load issued before.
-  cbs[cbi] = a.cb_is_table ? cbraw : (float)cbi;
+  if (a.cb_mode == CB_INLINE) {
+    float v = a.cbv[0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) v = cbi == j ? a.cbv[j] : v;
+    cbv = v;
+  }
+  cbs[cbi] = cbv;
   if constexpr (XM == XM_REG) {
     // unconditional stores (a thread past the end rewrites the last chunk
     // with the same bytes): a store under a predicate would let the compiler
     // sink its load next to it, past the weight loads, and drain them there
 #pragma unroll
-    for (int i = 0; i < XREG_CHUNKS; ++i) {
+    for (int i = 0; i < XRC; ++i) {
       const uint32_t c = min((uint32_t)(tid + i * NT), xch8 - 1u);
       const uint32_t m = c / kch, k = (c - m * kch) * 8u;
       *reinterpret_cast<ts_u32x4*>(xs + m * kK + k) = k < (uint32_t)a.cols ? xr[i] : ts_u32x4{0u, 0u, 0u, 0u};
@@ -607,7 +637,8 @@ inline size_t decode_smem(int M, int64_t K, bool xlds) {
 
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
           bool LOOP>
-inline int launch_decode_x(const DecodeArgs& a, hipStream_t st) {
+inline int launch_decode_x(const DecodeGroup& g, hipStream_t st) {
+  const DecodeArgs& a = g.a[0];
   const size_t smem = decode_smem<BITS, CB8, RVQ, REP, W>(a.M, a.K, XM != XM_GLOBAL);
   auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, LOOP>;
   static bool attr_set = false;
@@ -619,7 +650,7 @@ inline int launch_decode_x(const DecodeArgs& a, hipStream_t st) {
   }
   // one workgroup per 16-row tile; tiles beyond the resident capacity are
   // scheduled by the hardware as workgroups retire
-  hipLaunchKernelGGL(kern, dim3((unsigned)a.n_tiles), dim3(64 * W), smem, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)g.tile_end[g.n - 1]), dim3(64 * W), smem, st, g);
   TS_CHECK_LAUNCH();
   return TS_OK;
 }
@@ -648,27 +679,36 @@ inline DecShape decode_shape(int64_t n_tiles, int64_t G, int umax) {
 // when every batch is aligned, and the straight-line shape above; the rest
 // (x too large for LDS, unaligned metadata, rows longer than 32 batches of
 // the largest U) stream through the looping kernel.
+// The layers of a group share bits, group size, K, M, codebook kind and
+// double-quant kind (the caller checks); the launch shape is chosen for the
+// group's total tile count.
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP>
-inline int launch_decode(const DecodeArgs& a, hipStream_t st) {
+inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   constexpr int UMAX = DecGeom<BITS, GS, RVQ>::UMAX;
+  const DecodeArgs& a = g.a[0];
   const bool xlds = (size_t)a.M * a.K * 2 <= DEC_XLDS_MAX;
   const bool dq = a.dqsc != nullptr;
-  if (dq && a.dq_gs < (uint32_t)UMAX) return TS_NOT_COVERED;  // a batch would span > 2 super-groups
+  for (int l = 0; l < g.n; ++l)
+    if (dq && g.a[l].dq_gs < (uint32_t)UMAX) return TS_NOT_COVERED;  // a batch would span > 2 super-groups
   auto aligned_ptr = [](const void* p, size_t al) { return (reinterpret_cast<uintptr_t>(p) % al) == 0; };
   // aligned for batches of u groups: whole batches per row, and metadata base
-  // pointers aligned for u-wide (codes) / 2u-wide (f16) vector loads
+  // pointers aligned for u-wide (codes) / 2u-wide (f16) vector loads, in
+  // every layer
   auto aligned = [&](int u) {
     bool al = a.n_groups % u == 0;
-    if (dq) al = al && aligned_ptr(a.dqsc, u) && aligned_ptr(a.dqgc, u);
-    else al = al && aligned_ptr(a.scale, 2 * u) && aligned_ptr(a.gmin, 2 * u);
-    if (RVQ) al = al && aligned_ptr(a.s2scale, 2 * u) && aligned_ptr(a.s2gmin, 2 * u);
+    for (int l = 0; l < g.n; ++l) {
+      const DecodeArgs& b = g.a[l];
+      if (dq) al = al && aligned_ptr(b.dqsc, u) && aligned_ptr(b.dqgc, u);
+      else al = al && aligned_ptr(b.scale, 2 * u) && aligned_ptr(b.gmin, 2 * u);
+      if (RVQ) al = al && aligned_ptr(b.s2scale, 2 * u) && aligned_ptr(b.s2gmin, 2 * u);
+    }
     return al;
   };
-  const DecShape sh = decode_shape(a.n_tiles, a.n_groups, UMAX);
-  // x through registers when XREG_CHUNKS chunks per thread hold it
-  auto xreg = [&](int w) { return xlds && (int64_t)a.M * a.K / 8 <= (int64_t)XREG_CHUNKS * 64 * w; };
+  const DecShape sh = decode_shape(g.tile_end[g.n - 1], a.n_groups, UMAX);
+  // x through registers when xreg_chunks(w) chunks per thread hold it
+  auto xreg = [&](int w) { return xlds && (int64_t)a.M * a.K / 8 <= (int64_t)xreg_chunks(w) * 64 * w; };
 #define TS_DEC(XMV, DQV, ALV, WV, UV, LP) \
-  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, LP>(a, st)
+  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, LP>(g, st)
 #define TS_DEC_ALL(DQV)                                                          \
   do {                                                                           \
     const bool alm = aligned(UMAX);                                              \
@@ -697,17 +737,17 @@ inline int launch_decode(const DecodeArgs& a, hipStream_t st) {
 
 // Per-(bit width, group size) launchers, one translation unit each
 // (ts_decode_b<bits>_g<gs>.hip).
-int decode_b2_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b2_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b2_g256(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b4_g32(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b4_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b4_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b4_g256(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b6_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b6_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b8_g32(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b8_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
-int decode_b8_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st);
+int decode_b2_g64(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b2_g128(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b2_g256(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b4_g32(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b4_g64(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b4_g128(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b4_g256(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b6_g64(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b6_g128(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b8_g32(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b8_g64(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
+int decode_b8_g128(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st);
 
 }  // namespace ts

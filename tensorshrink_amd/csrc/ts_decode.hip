@@ -4,9 +4,11 @@
 
 namespace ts {
 
-int decode_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
-                   int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st) {
-  DecodeArgs a{};
+// Kernel arguments of one layer; NOT_COVERED when it has outliers but no
+// per-tile outlier slots.
+static int fill_args(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, void* y, int64_t ldy,
+                     int y_dtype, const uint16_t* bias, DecodeArgs& a) {
+  a = DecodeArgs{};
   a.packed = L->packed;
   a.pstride = L->packed_stride;
   a.scale = L->scale;
@@ -29,7 +31,10 @@ int decode_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx
   a.slots = has_out ? L->tile_outliers : static_cast<const uint64_t*>(dummy);
   a.cap = has_out ? (int32_t)L->tile_outlier_cap : 0;
   a.cbsrc = L->codebook ? L->codebook : static_cast<const float*>(dummy);
-  a.cb_is_table = L->codebook ? 1 : 0;
+  const int ncb = 1 << (L->bits == 6 ? 4 : L->bits);
+  a.cb_mode = !L->codebook ? CB_UNIFORM : (L->codebook_host && ncb <= 16) ? CB_INLINE : CB_DEVICE;
+  if (a.cb_mode == CB_INLINE)
+    for (int j = 0; j < 16; ++j) a.cbv[j] = L->codebook_host[j < ncb ? j : 0];
   a.x = x;
   a.ldx = ldx;
   a.y = y;
@@ -44,22 +49,62 @@ int decode_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx
   a.n_groups = L->n_groups;
   a.n_tiles = ts_cdiv(L->rows, 16);
   a.M = (int)M;
-  const bool bf16 = x_dtype == TS_BF16;
+  return TS_OK;
+}
+
+static int dispatch(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st) {
   switch (L->bits * 1000 + L->group_size) {
-    case 2064: return decode_b2_g64(L, a, bf16, st);
-    case 2128: return decode_b2_g128(L, a, bf16, st);
-    case 2256: return decode_b2_g256(L, a, bf16, st);
-    case 4032: return decode_b4_g32(L, a, bf16, st);
-    case 4064: return decode_b4_g64(L, a, bf16, st);
-    case 4128: return decode_b4_g128(L, a, bf16, st);
-    case 4256: return decode_b4_g256(L, a, bf16, st);
-    case 6064: return decode_b6_g64(L, a, bf16, st);
-    case 6128: return decode_b6_g128(L, a, bf16, st);
-    case 8032: return decode_b8_g32(L, a, bf16, st);
-    case 8064: return decode_b8_g64(L, a, bf16, st);
-    case 8128: return decode_b8_g128(L, a, bf16, st);
+    case 2064: return decode_b2_g64(L, g, bf16, st);
+    case 2128: return decode_b2_g128(L, g, bf16, st);
+    case 2256: return decode_b2_g256(L, g, bf16, st);
+    case 4032: return decode_b4_g32(L, g, bf16, st);
+    case 4064: return decode_b4_g64(L, g, bf16, st);
+    case 4128: return decode_b4_g128(L, g, bf16, st);
+    case 4256: return decode_b4_g256(L, g, bf16, st);
+    case 6064: return decode_b6_g64(L, g, bf16, st);
+    case 6128: return decode_b6_g128(L, g, bf16, st);
+    case 8032: return decode_b8_g32(L, g, bf16, st);
+    case 8064: return decode_b8_g64(L, g, bf16, st);
+    case 8128: return decode_b8_g128(L, g, bf16, st);
     default: return TS_NOT_COVERED;
   }
+}
+
+int decode_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
+                   int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st) {
+  DecodeGroup g{};
+  const int rc = fill_args(L, x, M, ldx, y, ldy, y_dtype, bias, g.a[0]);
+  if (rc != TS_OK) return rc;
+  g.tile_end[0] = g.a[0].n_tiles;
+  g.n = 1;
+  return dispatch(L, g, x_dtype == TS_BF16, st);
+}
+
+// Layers that can share one launch: the same bit width, group size, column
+// count, padding, codebook kind, double-quant kind and stage-2 kind.
+static bool same_format(const ts_qlayer* a, const ts_qlayer* b) {
+  return a->bits == b->bits && a->group_size == b->group_size && a->cols == b->cols &&
+         a->padded_cols == b->padded_cols && a->n_groups == b->n_groups &&
+         (a->codebook != nullptr) == (b->codebook != nullptr) &&
+         (a->dq_scale_codes != nullptr) == (b->dq_scale_codes != nullptr) &&
+         (a->stage2_packed != nullptr) == (b->stage2_packed != nullptr);
+}
+
+int decode_forward_group(const ts_qlayer* const* layers, int n, const uint16_t* x, int64_t M, int64_t ldx,
+                         int x_dtype, void* const* y, const int64_t* ldy, int y_dtype,
+                         const uint16_t* const* bias, hipStream_t st) {
+  if (n < 1 || n > DEC_GMAX) return TS_NOT_COVERED;
+  DecodeGroup g{};
+  int64_t tiles = 0;
+  for (int l = 0; l < n; ++l) {
+    if (!same_format(layers[0], layers[l])) return TS_NOT_COVERED;
+    const int rc = fill_args(layers[l], x, M, ldx, y[l], ldy[l], y_dtype, bias ? bias[l] : nullptr, g.a[l]);
+    if (rc != TS_OK) return rc;
+    tiles += g.a[l].n_tiles;
+    g.tile_end[l] = tiles;
+  }
+  g.n = n;
+  return dispatch(layers[0], g, x_dtype == TS_BF16, st);
 }
 
 }  // namespace ts

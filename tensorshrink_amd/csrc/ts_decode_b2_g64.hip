@@ -4,9 +4,9 @@
 
 namespace ts {
 
-int decode_b2_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st) {
+int decode_b2_g64(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st) {
   (void)L;
-  return bf16 ? launch_decode<2, 64, true, false, false, 4>(a, st) : launch_decode<2, 64, false, false, false, 4>(a, st);
+  return bf16 ? launch_decode<2, 64, true, false, false, 4>(g, st) : launch_decode<2, 64, false, false, false, 4>(g, st);
 }
 
 }  // namespace ts

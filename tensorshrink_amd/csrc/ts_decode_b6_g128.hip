@@ -5,9 +5,9 @@
 
 namespace ts {
 
-int decode_b6_g128(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st) {
+int decode_b6_g128(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st) {
   (void)L;
-  return bf16 ? launch_decode<4, 128, true, false, true, 4>(a, st) : launch_decode<4, 128, false, false, true, 4>(a, st);
+  return bf16 ? launch_decode<4, 128, true, false, true, 4>(g, st) : launch_decode<4, 128, false, false, true, 4>(g, st);
 }
 
 }  // namespace ts

@@ -6,11 +6,11 @@
 
 namespace ts {
 
-int decode_b8_g64(const ts_qlayer* L, DecodeArgs& a, bool bf16, hipStream_t st) {
+int decode_b8_g64(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st) {
   (void)L;
   if (L->codebook)
-    return bf16 ? launch_decode<8, 64, true, true, false, 16>(a, st) : launch_decode<8, 64, false, true, false, 16>(a, st);
-  return bf16 ? launch_decode<8, 64, true, false, false, 1>(a, st) : launch_decode<8, 64, false, false, false, 1>(a, st);
+    return bf16 ? launch_decode<8, 64, true, true, false, 16>(g, st) : launch_decode<8, 64, false, true, false, 16>(g, st);
+  return bf16 ? launch_decode<8, 64, true, false, false, 1>(g, st) : launch_decode<8, 64, false, false, false, 1>(g, st);
 }
 
 }  // namespace ts

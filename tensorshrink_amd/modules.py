@@ -22,7 +22,7 @@ Additions over the reference:
 from __future__ import annotations
 
 import ctypes
-from typing import Iterable, Optional, Tuple, Union
+from typing import Iterable, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 import torch
@@ -161,6 +161,9 @@ class QuantLinear(nn.Module):
             s.gmin = self.gmin.data_ptr()
         if self.companded:
             s.codebook = self.codebook.data_ptr()
+            # host copy kept alive with the view (decode takes <= 16 entries as launch arguments)
+            self._codebook_host = np.ascontiguousarray(self.codebook.detach().cpu().numpy(), dtype=np.float32)
+            s.codebook_host = self._codebook_host.ctypes.data
         if self.bits == 6:
             s.stage2_packed = self.stage2_packed.data_ptr()
             s.stage2_stride = self.stage2_packed.shape[1]
@@ -287,6 +290,41 @@ class QuantLinear(nn.Module):
                                             y.data_ptr(), self.out_features, dt, L.ptr(b), None, 0,
                                             L.stream_ptr(x.device)), "qlinear forward")
         return y.reshape(*lead, self.out_features)
+
+    @staticmethod
+    def forward_group(layers: Sequence["QuantLinear"], x: torch.Tensor) -> List[torch.Tensor]:
+        """[layer(x) for layer in layers] in one kernel launch when the layers
+        share a format and the input has at most 16 rows (q/k/v or gate/up at
+        decode); otherwise, or when the launch is not covered, one forward per
+        layer. No counterpart in the reference, whose model code calls each
+        QuantLinear in turn (modules.py:896-905)."""
+        layers = list(layers)
+        in_dtype = x.dtype
+        M = 1
+        for d in x.shape[:-1]:
+            M *= d
+        ok = (1 <= len(layers) <= 4 and M <= 16 and x.is_cuda and in_dtype in (torch.float16, torch.bfloat16)
+              and all(q._layer is not None and not q.force_fp32_compute and q.in_features == layers[0].in_features
+                      for q in layers))
+        if ok:
+            lead = x.shape[:-1]
+            x2d = x.reshape(M, layers[0].in_features)
+            if not x2d.is_contiguous():
+                x2d = x2d.contiguous()
+            ys = [torch.empty(M, q.out_features, dtype=in_dtype, device=x.device) for q in layers]
+            bs = [q._bias_as(in_dtype) for q in layers]
+            n = len(layers)
+            qls = (ctypes.POINTER(L.QLayer) * n)(*[ctypes.pointer(q._layer) for q in layers])
+            yp = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
+            ld = (ctypes.c_int64 * n)(*[q.out_features for q in layers])
+            bp = (ctypes.c_void_p * n)(*[L.ptr(b) for b in bs])
+            dt = L.dtype_code(in_dtype)
+            rc = L.load().ts_qlinear_forward_group(qls, n, x2d.data_ptr(), M, layers[0].in_features, dt, yp, ld, dt,
+                                                   bp, L.stream_ptr(x.device))
+            if rc != L.TS_NOT_COVERED:
+                L.check(rc, "qlinear group forward")
+                return [y.reshape(*lead, q.out_features) for y, q in zip(ys, layers)]
+        return [q(x) for q in layers]
 
     @classmethod
     def from_linear(cls, linear: nn.Linear, bits: int = 4, group_size: int = 128, outlier_frac: float = 0.001,

@@ -167,3 +167,38 @@ def test_kernel_api_functions():
     mask = torch.ones(W.numel(), dtype=torch.bool, device="cuda")
     mask[torch.from_numpy(d["qt_outlier_idx"].astype(np.int64)).cuda()] = False
     assert torch.equal(Wq.reshape(-1)[mask], W.reshape(-1)[mask])
+
+
+@pytest.mark.parametrize("opts", [NF4, dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True,
+                                            nf_quant=True),
+                                  dict(bits=6, group_size=64, outlier_frac=0.002, double_quant=False)])
+def test_forward_group_matches_single(opts):
+    """QuantLinear.forward_group (one launch for layers sharing x) against the
+    per-layer forward and the float32 reference."""
+    ts = _ts()
+    shapes = [(512, 1024), (128, 1024), (136, 1024)]
+    made = [_layer(n, k, 70 + i, opts) for i, (n, k) in enumerate(shapes)]
+    qls = [m[0] for m in made]
+    torch.manual_seed(0)
+    qls[1].bias = torch.randn(qls[1].out_features, dtype=torch.bfloat16).cuda()
+    for M in (1, 5, 16):
+        x = recipes.activations(M, 1024, seed=M).cuda()
+        ys = ts.QuantLinear.forward_group(qls, x)
+        for q, (ql, W), y in zip(qls, made, ys):
+            y1 = ql(x)
+            assert y.shape == y1.shape and y.dtype == y1.dtype
+            assert max_rel_err(y.float(), y1.float()) <= 1e-3
+            ref = x.float() @ W.T + (ql.bias.float() if ql.bias is not None else 0)
+            assert max_rel_err(y.float(), ref) <= TOL
+
+
+def test_forward_group_fallbacks():
+    """Mixed formats and M > 16 run one forward per layer."""
+    ts = _ts()
+    a, Wa = _layer(256, 512, 81, NF4)
+    b, Wb = _layer(256, 512, 82, dict(bits=8, group_size=128, outlier_frac=0.0, double_quant=False))
+    for M in (3, 40):
+        x = recipes.activations(M, 512, seed=M).cuda()
+        ya, yb = ts.QuantLinear.forward_group([a, b], x)
+        assert max_rel_err(ya.float(), x.float() @ Wa.T) <= TOL
+        assert max_rel_err(yb.float(), x.float() @ Wb.T) <= TOL
