@@ -12,8 +12,9 @@ one layer forward: the seven QuantLinear forwards in four launches, q/k/v and
 gate/up each one grouped launch over layers that share their input
 (QuantLinear.forward_group), o and down one launch each (--ungrouped: seven
 launches). Ten copies of the layer (1.2 GB) are rotated so every step streams
-its weights from HBM and not from the 256 MB MALL; each copy's step is a
-captured HIP graph.
+its weights from HBM and not from the 256 MB MALL: one captured HIP graph
+holds ten consecutive steps, one per copy, as a ten-layer model's decode
+graph would.
 
 Alongside it (extra keys of the same JSON line):
   * "roofline"     - the decode kernel: algorithmic bytes of a step's launches /
@@ -116,37 +117,44 @@ def bench_decode(args, opts):
     step_bytes = sum(layer_bytes(q, 1) for _, q in base)
     units = SINGLE_UNITS if args.ungrouped else GROUPED_UNITS
     stream = torch.cuda.Stream()
-    graphs, outs = [], []
+    C = len(copies)
+    full, rem = divmod(args.steps, C)
+    outs = []
     with torch.cuda.stream(stream):
         for layer in copies:  # warm every kernel instantiation outside capture
             for _, idx in units:
                 run_unit(layer, idx, xs)
         torch.cuda.synchronize()
-        for layer in copies:
+
+        def capture(n):  # one graph: n consecutive steps, step i on copy i
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, stream=stream):
-                outs.append([run_unit(layer, idx, xs) for _, idx in units])
-            graphs.append(g)
+                for layer in copies[:n]:
+                    outs.append([run_unit(layer, idx, xs) for _, idx in units])
+            return g
+        g_all = capture(C)
+        g_rem = capture(rem) if rem else None
         torch.cuda.synchronize()
-        for s in range(args.warmup):
-            graphs[s % len(graphs)].replay()
+        for _ in range(max(1, -(-args.warmup // C))):
+            g_all.replay()
         torch.cuda.synchronize()
-        # timed region: exactly K steps; HIP events around every replay on the
-        # replay stream (replays are queued faster than they run, so the
-        # stream stays busy and each event pair brackets one step's kernels)
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(args.steps)]
+        # timed region: exactly K steps, as K // C replays of the C-step graph
+        # and one of a K % C-step graph; HIP events around each replay on the
+        # replay stream
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True), C)
+               for _ in range(full)]
+        if rem:
+            evs.append((torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True), rem))
         t0 = time.perf_counter()
-        for s in range(args.steps):
-            evs[s][0].record(stream)
-            graphs[s % len(graphs)].replay()
-            evs[s][1].record(stream)
+        for i, (e0, e1, n) in enumerate(evs):
+            e0.record(stream)
+            (g_all if n == C else g_rem).replay()
+            e1.record(stream)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    gpu_ms = [a.elapsed_time(b) for a, b in evs[1:]]  # the first pair starts on an idle queue
-    step_gpu_ms = sum(gpu_ms) / len(gpu_ms)
+    step_gpu_ms = sum(a.elapsed_time(b) for a, b, _ in evs) / args.steps
     kern = unit_kernel_time(copies, xs, stream, units, reps=args.kernel_reps)
     return dict(ms_per_step=ms_per_step, value=value, step_bytes=step_bytes, kern=kern,
                 base=base, xs=xs, step_gpu_us=step_gpu_ms * 1e3, units=units)
