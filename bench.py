@@ -14,7 +14,9 @@ gate/up each one grouped launch over layers that share their input
 launches). Ten copies of the layer (1.2 GB) are rotated so every step streams
 its weights from HBM and not from the 256 MB MALL: one captured HIP graph
 holds ten consecutive steps, one per copy, as a ten-layer model's decode
-graph would.
+graph would. Each launch reads the activation the launch before it wrote (of
+the width it needs; the first launch of a replay reads a resident input), as
+every linear of a decoder layer does.
 
 Alongside it (extra keys of the same JSON line):
   * "roofline"     - the decode kernel: algorithmic bytes of a step's launches /
@@ -98,14 +100,24 @@ GROUPED_UNITS = [("qkv", (0, 1, 2)), ("o", (3,)), ("gate_up", (4, 5)), ("down", 
 SINGLE_UNITS = [(n, (i,)) for i, n in enumerate(("q", "k", "v", "o", "gate", "up", "down"))]
 
 
-def run_unit(layer, idx, xs):
-    """The forwards of one launch unit (a list of outputs)."""
+def run_unit(layer, idx, xs, live=None):
+    """The forwards of one launch unit (a list of outputs). With `live`, the
+    input is the latest output of the input's width (the activation the
+    previous launch just wrote, as in a model's decode step, where every
+    linear reads what the kernel before it produced), and the unit's outputs
+    become the latest of their widths."""
     import tensorshrink_amd as ts
     qs = [layer[i][1] for i in idx]
-    x = xs[qs[0].in_features]
-    if len(qs) == 1:
-        return [qs[0](x)]
-    return ts.QuantLinear.forward_group(qs, x)
+    src = live if live is not None else xs
+    x = src[qs[0].in_features]
+    ys = [qs[0](x)] if len(qs) == 1 else ts.QuantLinear.forward_group(qs, x)
+    if live is not None:
+        seen = set()
+        for y in ys:
+            if y.shape[-1] not in seen:
+                live[y.shape[-1]] = y
+                seen.add(y.shape[-1])
+    return ys
 
 
 def bench_decode(args, opts):
@@ -126,11 +138,12 @@ def bench_decode(args, opts):
                 run_unit(layer, idx, xs)
         torch.cuda.synchronize()
 
-        def capture(n):  # one graph: n consecutive steps, step i on copy i
+        def capture(n):  # one graph: n consecutive steps, step i on copy i, chained
             g = torch.cuda.CUDAGraph()
+            live = dict(xs)
             with torch.cuda.graph(g, stream=stream):
                 for layer in copies[:n]:
-                    outs.append([run_unit(layer, idx, xs) for _, idx in units])
+                    outs.append([run_unit(layer, idx, xs, live) for _, idx in units])
             return g
         g_all = capture(C)
         g_rem = capture(rem) if rem else None
@@ -161,10 +174,11 @@ def bench_decode(args, opts):
 
 
 def unit_kernel_time(copies, xs, stream, units, reps: int):
-    """Average decode launch duration per launch unit: one graph per unit
-    holding that unit's launch on every copy (back to back, the weights
-    rotating so none comes from the MALL), replayed `reps` times between two
-    HIP events on the launch stream. The per-launch average includes the
+    """Average decode launch duration per launch unit in isolation: one graph
+    per unit holding that unit's launch on every copy (back to back, the
+    weights rotating so none comes from the MALL, x a resident tensor that
+    the weight stream evicts from the caches), replayed `reps` times between
+    two HIP events on the launch stream. The per-launch average includes the
     dispatch gap between consecutive kernels of a graph."""
     out = {}
     with torch.cuda.stream(stream):
@@ -341,9 +355,9 @@ def main():
     dec = bench_decode(args, opts)
     kern = dec["kern"]
     k_us = sum(v["us"] for v in kern.values())
-    achieved = dec["step_bytes"] / (k_us * 1e-6) / 1e9
-    log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s; kernel launches "
-        f"{k_us:.1f} us/layer -> {achieved:.0f} GB/s")
+    achieved = dec["step_bytes"] / (dec["step_gpu_us"] * 1e-6) / 1e9
+    log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s; GPU {dec['step_gpu_us']:.1f} "
+        f"us/step -> {achieved:.0f} GB/s; isolated launches (resident x) {k_us:.1f} us/layer")
     traffic = load_traffic(dec["units"])
     pre = None
     if not args.no_prefill:
@@ -376,12 +390,13 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic["bytes_per_step"] if traffic else None,
-                     "kernel": "ts::decode_kernel (4-bit NF4 + DQ, group 128, bf16); achieved = algorithmic "
-                               "bytes of a step's launches / sum of their average launch durations (HIP events "
-                               "around graph replays of each launch over the 10 copies); traffic = HBM bytes "
-                               "of those launches (PMC)",
-                     "launch_us_per_layer": round(k_us, 2), "step_gpu_us": round(dec["step_gpu_us"], 2),
-                     "per_launch": kern,
+                     "kernel": "ts::decode_kernel (4-bit NF4 + DQ, group 128, bf16), the only kernel of a "
+                               "step; achieved = algorithmic bytes of a step's launches / their GPU time (HIP "
+                               "events on the launch stream around each replay of the timed region, per step); "
+                               "traffic = HBM bytes of those launches (PMC)",
+                     "step_gpu_us": round(dec["step_gpu_us"], 2),
+                     "isolated_launch_us_per_layer": round(k_us, 2),
+                     "per_launch_isolated": kern,
                      "traffic_per_launch": traffic["per_launch_bytes"] if traffic else None},
         "prefill": pre,
         "cpu_baseline": cpu,

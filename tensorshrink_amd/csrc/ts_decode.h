@@ -480,19 +480,6 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // that point needs anyway.
   float cbv = (float)cbi;  // uniform grid
   if (a.cb_mode == CB_DEVICE) cbv = a.cbsrc[cbi < NCB ? cbi : 0];
-  Batch bufA, bufB;
-  load_batch(tile, 0, bufA);
-  load_batch(tile, 1, bufB);  // (a dead batch when nb == 1)
-  // This tile's outlier slots sit at a fixed address (no dependent load):
-  // each thread takes slots tid and tid + NT; more (rare) are read in the
-  // epilogue. Indices past cap read a valid slot whose value is dropped.
-  const int64_t sbase = tile * a.cap;
-  const int capm1 = max(a.cap - 1, 0);
-  const uint64_t slot0 = a.slots[sbase + min(tid, capm1)];
-  const uint64_t slot1 = a.slots[sbase + min(tid + NT, capm1)];
-  // bias of the output this thread stores (16 rows x M; entry 0 of a valid
-  // array when there is no bias)
-  const uint16_t bias_v = a.bias_src[min(r0 + (tid & 15), a.N - 1) * a.bias_mul];
 
   // unconditional store (threads tid, tid + 256, ... write the same value to
   // slot tid % 256): a store under `tid < NCB` would let the compiler sink
@@ -530,6 +517,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     asm volatile("" ::"v"(last));
     if (kK > (uint32_t)a.cols) {  // column padding: x is zero there
       __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): all of this wave's chunks landed
+      // a row's padding may sit in another wave's chunk: zero it only once
+      // every wave's chunks have landed, or a late chunk overwrites the zeros
+      ts_lds_barrier();
       const uint32_t padw = kK - (uint32_t)a.cols;
       for (uint32_t e = tid; e < (uint32_t)a.M * padw; e += NT) {
         const uint32_t m = e / padw;
@@ -558,6 +548,28 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
   }
   ts_lds_barrier();
+
+  // The weight stream starts only now, after the workgroup's barriers: a
+  // barrier behind it would wait until every wave had issued all its loads,
+  // which under a full memory pipeline is most of the stream, and no wave
+  // could compute before then. From here on each wave computes a batch as
+  // soon as its own loads land.
+  Batch bufA, bufB;
+  load_batch(tile, 0, bufA);
+  load_batch(tile, 1, bufB);  // (a dead batch when nb == 1)
+  // This tile's outlier slots sit at a fixed address (no dependent load):
+  // each thread takes slots tid and tid + NT; more (rare) are read in the
+  // epilogue. Indices past cap read a valid slot whose value is dropped.
+  const int64_t sbase = tile * a.cap;
+  const int capm1 = max(a.cap - 1, 0);
+  const uint64_t slot0 = a.slots[sbase + min(tid, capm1)];
+  const uint64_t slot1 = a.slots[sbase + min(tid + NT, capm1)];
+  // bias of the output this thread stores (16 rows x M; entry 0 of a valid
+  // array when there is no bias)
+  const uint16_t bias_v = a.bias_src[min(r0 + (tid & 15), a.N - 1) * a.bias_mul];
+  // every load above stays here (the compiler would otherwise sink batch B's
+  // loads into its conditional compute step and drain the counter there)
+  asm volatile("" ::: "memory");
 
   // Two register buffers, bound statically (a runtime-indexed pair would live
   // in scratch memory). Without LOOP both were issued in the prologue (the
