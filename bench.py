@@ -213,16 +213,14 @@ def unit_kernel_time(copies, xs, stream, units, reps: int):
 def load_traffic(units):
     """HBM bytes per launch from the committed PMC summary (FETCH_SIZE and
     WRITE_SIZE passes of rocprofv3 over this bench, each scaled by the same
-    counter's reading for a plain copy of known size), or None. A grouped
-    launch is the sum of its layers' launches."""
+    counter's reading for a plain copy of known size), or None when the
+    summary does not cover these launch units."""
     path = os.path.join(ROOT, "profiles", "decode_traffic.json")
     if not os.path.exists(path):
         return None
-    names = ("q", "k", "v", "o", "gate", "up", "down")
     try:
-        t = json.load(open(path))
-        per = t["per_linear_bytes"]
-        pu = {u: int(sum(per[names[i]] for i in idx)) for u, idx in units}
+        per = json.load(open(path))["per_launch_bytes"]
+        pu = {u: int(per[u]) for u, _ in units}
         return {"bytes_per_step": int(sum(pu.values())), "per_launch_bytes": pu,
                 "source": "profiles/decode_traffic.json"}
     except (OSError, KeyError, ValueError):
