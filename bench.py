@@ -24,6 +24,9 @@ Alongside it (extra keys of the same JSON line):
                      graph replays of each launch over the copies), vs 8 TB/s;
   * "prefill"      - BASELINE config 4: gate/up/down at M=2048, 8-bit NF8 + DQ
                      and 6-bit RVQ, 2*M*N*K flops / kernel time vs 2.5 PFLOP/s;
+  * "quantize"     - BASELINE config 5's GPU GOAP quantize (28672x8192) through
+                     the public API, wall time, with the oracle CPU codec timed
+                     on a slice;
   * "cpu_baseline" - the reference CPU fallback forward (bf16 dequant + F.linear,
                      modules.py:752-804, 924-940), restated in oracle/, timed
                      on this host's cores for one layer forward at M=1.
@@ -278,6 +281,55 @@ def bench_prefill(args):
     return res
 
 
+def bench_quantize(args):
+    """BASELINE config 5's GPU GOAP quantize: the 28672x8192 fp16 N(0, 0.015)
+    weight with outliers, 4-bit uniform, group 128, outlier_frac 0.001 (the
+    gpu_quantize.py flavour), through the public API (quantize_tensor returns
+    host numpy arrays, as the reference's does). Wall time per call with the
+    weight resident on the GPU; algorithmic bytes = read N*K*2 + write packed
+    + scale/gmin + outliers (i32 index + fp16 value). The reference CPU codec,
+    restated in oracle/ (libstdc++ top-k + numpy), is timed on a 2048-row
+    slice of the same weight on this host's cores."""
+    import numpy as np
+    import recipes
+    import tensorshrink_amd as ts
+    from oracle import codec_ref as O
+    N, K, gs, frac = 28672, 8192, 128, 0.001
+    w = recipes.gaussian_weight(N, K, 5005, sigma=0.015).cuda()
+    opts = dict(bits=4, group_size=gs, outlier_frac=frac)
+    ts.quantize_tensor(w, **opts)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.quantize_reps):
+        t0 = time.perf_counter()
+        qt = ts.quantize_tensor(w, **opts)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    k = max(1, int(N * K * frac))
+    nbytes = N * K * 2 + qt.packed.nbytes + qt.scale.nbytes + qt.gmin.nbytes + k * (4 + 2)
+    res = {"workload": "GOAP quantize 28672x8192 fp16 -> 4-bit uniform, group 128, outlier_frac 0.001 "
+                       "(BASELINE config 5), host numpy result",
+           "ms": round(med * 1e3, 2), "bytes": nbytes, "GBps": round(nbytes / med / 1e9, 2),
+           "frac_of_hbm_peak": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 5)}
+    if not args.no_cpu:
+        rows = 2048
+        ws = w[:rows].cpu()
+        torch.set_num_threads(os.cpu_count() or 1)
+        t0 = time.perf_counter()
+        O.quantize(ws, bits=4, group_size=gs, outlier_frac=frac)
+        t = time.perf_counter() - t0
+        sb = rows * K * 2 + rows * K // 2 + 2 * rows * (K // gs) * 2 + int(rows * K * frac) * 6
+        res["cpu_baseline"] = {"value": round(sb / t / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "ms": round(t * 1e3, 1),
+                               "sample": f"oracle CPU quantize of rows 0..{rows - 1} of the same weight "
+                                         f"({rows}x{K}), one call"}
+    del w
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(dec, budget_s: float):
     """Time the reference CPU fallback forward (oracle restatement) for one
     layer at M=1, on this host's cores, with the layer's own codes."""
@@ -337,6 +389,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--ungrouped", action="store_true", help="one launch per linear (7 per step)")
+    ap.add_argument("--no-quantize", action="store_true")
+    ap.add_argument("--quantize-reps", type=int, default=3)
     ap.add_argument("--copy-calib", action="store_true", help="only run the plain-copy PMC calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -362,6 +416,11 @@ def main():
         log("prefill: M=2048")
         pre = bench_prefill(args)
         log(f"prefill: {pre}")
+    quant = None
+    if not args.no_quantize:
+        log("quantize: 28672x8192")
+        quant = bench_quantize(args)
+        log(f"quantize: {quant}")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -397,6 +456,7 @@ def main():
                      "per_launch_isolated": kern,
                      "traffic_per_launch": traffic["per_launch_bytes"] if traffic else None},
         "prefill": pre,
+        "quantize": quant,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
