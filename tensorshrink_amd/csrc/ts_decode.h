@@ -4,36 +4,38 @@
 // (triton_kernels.py:278-541, dispatched at modules.py:881-894) and its
 // standalone outlier pass (triton_kernels.py:543-576, 940-941).
 //
-// Work unit: a tile of 16 weight rows x all of K. A workgroup of 4 waves owns
-// a tile (persistent over tiles only when more tiles than resident workgroups);
-// wave w owns a contiguous run of the tile's group batches.
+// Work unit: a tile of 16 weight rows x all of K, one workgroup of W waves
+// (4, 8 or 16) per tile; wave w owns a contiguous run of the tile's group
+// batches. Layers that read the same x can share a launch (DecodeGroup).
 //   * MFMA f32_16x16x32 (bf16 or f16): lane l owns W row r0 + l%16 (B column)
 //     and x row l%16 (A row); lane group q = l/16 owns a quarter of each group,
 //     so one group is GS/32 MFMAs over that lane set.
-//   * Each lane streams its quarter-group of packed codes with 8/16-byte loads,
-//     U groups per batch, double-buffered in registers across batches and
-//     tiles. A batch's per-group metadata comes in a few vector loads: U
-//     scale/double-quant codes in one load when the batch is aligned, and the
-//     (at most two) double-quant super-groups it spans in four.
+//   * Each lane loads its quarter-group of packed codes with 8/16-byte loads,
+//     U groups per batch, two batches in registers. A batch's per-group
+//     metadata comes in a few vector loads: U scale/double-quant codes in one
+//     load when the batch is aligned, and the (at most two) double-quant
+//     super-groups it spans in four.
 //   * Codes become bf16/f16 pairs through an LDS table indexed by the packed
 //     byte (4-bit: one u32 = two codes; 2-bit: one u64 = four codes), kept in
-//     REP bank-private copies so random bytes never collide on a bank.
+//     bank-private copies (up to one per lane of a half-wave).
 //   * The per-group affine is factorised out of the MFMA:
 //         y += s[n,g] * (x . cb[c]) + gmin[n,g] * (x . 1)
 //     with both dot products on the matrix core and s/gmin in float32
 //     (rebuilt from double-quant codes in-register, modules.py:573-579).
 //   * x is staged once per workgroup in LDS when M*K fits, else read per group.
-//   * Per tile: the waves' partials reduced in LDS, the tile's row-sorted
-//     outliers (CSR slice, loaded one tile ahead) added with LDS float atomics,
-//     then bias and the compute-dtype store.
+//   * Per tile: the waves' partials reduced in LDS, the tile's outliers (its
+//     per-tile slots) added with LDS float atomics, then bias and the
+//     compute-dtype store.
 //
 // Latency rules the code follows (each was measured to matter on gfx950):
-//   * every load of a phase is issued before anything waits: loads are
+//   * kernel arguments are pinned in SGPRs at entry (one batch of scalar loads
+//     instead of several dependent ones);
+//   * the workgroup's barriers (x staging, code tables) come before the weight
+//     stream, so no barrier waits for every wave to have issued its loads;
+//   * every weight load is issued before anything waits: loads are
 //     unconditional (addresses clamped into valid memory, predicates applied
 //     where the value is used), since a load under a branch is followed by a
 //     wait at the join;
-//   * kernel arguments are pinned in SGPRs at entry (one batch of scalar loads
-//     instead of several dependent ones);
 //   * LDS barriers wait for LDS traffic only (ts_lds_barrier), never for the
 //     weight loads in flight.
 #pragma once
@@ -134,6 +136,12 @@ TS_DEV Bytes<NB> load_bytes(const uint8_t* p) {
 TS_DEV uint32_t byte_of(const uint32_t* d, int i) { return (d[i >> 2] >> (8 * (i & 3))) & 0xffu; }
 TS_DEV uint32_t half_of(const uint32_t* d, int i) { return (d[i >> 1] >> (16 * (i & 1))) & 0xffffu; }
 
+// Bank-private copies of a code table. REP = 32 asks for one copy per lane of
+// a half-wave (conflict-free lookups, 32 KB for a 4-bit table) where one
+// workgroup fills a CU (16 waves); with fewer waves per workgroup several
+// workgroups share the CU's LDS and get fewer copies.
+constexpr int dec_rep(int rep, int w) { return rep >= 32 ? (w >= 16 ? 32 : (w >= 8 ? 16 : 4)) : rep; }
+
 template <int BITS, int GS, bool RVQ>
 struct DecGeom {
   static constexpr int GB = GS * BITS / 8;  // packed bytes per row per group
@@ -167,6 +175,7 @@ template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool
           bool LOOP>
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) {
   constexpr int NT = 64 * W;
+  constexpr int R = dec_rep(REP, W);  // table copies
   constexpr bool XLDS = XM != XM_GLOBAL;
   extern __shared__ __align__(16) unsigned char smem[];
   using Geo = DecGeom<BITS, GS, RVQ>;
@@ -206,16 +215,16 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   const int wave = tid >> 6;
   const int n = lane & 15;
   const int q = lane >> 4;
-  const int rsl = lane & (REP - 1);
+  const int rsl = lane & (R - 1);
 
   // ---- LDS carve-up ------------------------------------------------------
   unsigned char* sp = smem;
   uint32_t* t4 = nullptr;
   uint2* t2 = nullptr;
   uint32_t* t8 = nullptr;
-  if constexpr (USE_T4) { t4 = reinterpret_cast<uint32_t*>(sp); sp += 256 * REP * 4; }
-  if constexpr (USE_T2) { t2 = reinterpret_cast<uint2*>(sp); sp += 256 * REP * 8; }
-  if constexpr (USE_T8) { t8 = reinterpret_cast<uint32_t*>(sp); sp += 256 * REP * 4; }
+  if constexpr (USE_T4) { t4 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
+  if constexpr (USE_T2) { t2 = reinterpret_cast<uint2*>(sp); sp += 256 * R * 8; }
+  if constexpr (USE_T8) { t8 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
   float* red = reinterpret_cast<float*>(sp);       // [W][64][4]
   sp += W * 64 * 4 * 4;
   float* ys = reinterpret_cast<float*>(sp);        // [16][17]
@@ -368,15 +377,15 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
         }
         if constexpr (BITS == 4) {
           const int b0 = 4 * j;
-          bv[j] = ts_u32x4{t4[byte_of(B.w[u].d, b0 + 0) * REP + rsl], t4[byte_of(B.w[u].d, b0 + 1) * REP + rsl],
-                           t4[byte_of(B.w[u].d, b0 + 2) * REP + rsl], t4[byte_of(B.w[u].d, b0 + 3) * REP + rsl]};
+          bv[j] = ts_u32x4{t4[byte_of(B.w[u].d, b0 + 0) * R + rsl], t4[byte_of(B.w[u].d, b0 + 1) * R + rsl],
+                           t4[byte_of(B.w[u].d, b0 + 2) * R + rsl], t4[byte_of(B.w[u].d, b0 + 3) * R + rsl]};
         } else if constexpr (BITS == 2) {
-          const uint2 e0 = t2[byte_of(B.w[u].d, 2 * j + 0) * REP + rsl];
-          const uint2 e1 = t2[byte_of(B.w[u].d, 2 * j + 1) * REP + rsl];
+          const uint2 e0 = t2[byte_of(B.w[u].d, 2 * j + 0) * R + rsl];
+          const uint2 e1 = t2[byte_of(B.w[u].d, 2 * j + 1) * R + rsl];
           bv[j] = ts_u32x4{e0.x, e0.y, e1.x, e1.y};
         } else if constexpr (CB8) {
-          bv[j] = ts_u32x4{t8[byte_of(B.w[u].d, 4 * j + 0) * REP + rsl], t8[byte_of(B.w[u].d, 4 * j + 1) * REP + rsl],
-                           t8[byte_of(B.w[u].d, 4 * j + 2) * REP + rsl], t8[byte_of(B.w[u].d, 4 * j + 3) * REP + rsl]};
+          bv[j] = ts_u32x4{t8[byte_of(B.w[u].d, 4 * j + 0) * R + rsl], t8[byte_of(B.w[u].d, 4 * j + 1) * R + rsl],
+                           t8[byte_of(B.w[u].d, 4 * j + 2) * R + rsl], t8[byte_of(B.w[u].d, 4 * j + 3) * R + rsl]};
         } else {
           uint32_t pr[4];
 #pragma unroll
@@ -392,8 +401,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
           bv[j] = ts_u32x4{pr[0], pr[1], pr[2], pr[3]};
         }
         if constexpr (RVQ) {
-          const uint2 e0 = t2[byte_of(B.w2[u].d, 2 * j + 0) * REP + rsl];
-          const uint2 e1 = t2[byte_of(B.w2[u].d, 2 * j + 1) * REP + rsl];
+          const uint2 e0 = t2[byte_of(B.w2[u].d, 2 * j + 0) * R + rsl];
+          const uint2 e1 = t2[byte_of(B.w2[u].d, 2 * j + 1) * R + rsl];
           bv2[j] = ts_u32x4{e0.x, e0.y, e1.x, e1.y};
         }
       }
@@ -528,8 +537,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
   }
   ts_lds_barrier();
-  for (int e = tid; e < 256 * REP; e += NT) {
-    const int b = e / REP;
+  for (int e = tid; e < 256 * R; e += NT) {
+    const int b = e / R;
     if constexpr (USE_T4) t4[e] = pack2<BF16>(cbs[b & 15], cbs[b >> 4]);
     if constexpr (USE_T2) {
       // RVQ stage 2 is always a uniform grid; a 2-bit layer uses its codebook.
@@ -636,10 +645,11 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
 
 template <int BITS, bool CB8, bool RVQ, int REP, int W>
 inline size_t decode_smem(int M, int64_t K, bool xlds) {
+  constexpr int R = dec_rep(REP, W);
   size_t s = 0;
-  if (BITS == 4) s += 256 * REP * 4;
-  if (BITS == 2 || RVQ) s += 256 * REP * 8;
-  if (BITS == 8 && CB8) s += 256 * REP * 4;
+  if (BITS == 4) s += 256 * R * 4;
+  if (BITS == 2 || RVQ) s += 256 * R * 8;
+  if (BITS == 8 && CB8) s += 256 * R * 4;
   s += (size_t)W * 64 * 16;
   s += 16 * 17 * 4;
   s += 256 * 4;

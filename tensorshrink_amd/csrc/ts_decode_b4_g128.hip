@@ -6,7 +6,7 @@ namespace ts {
 
 int decode_b4_g128(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t st) {
   (void)L;
-  return bf16 ? launch_decode<4, 128, true, false, false, 4>(g, st) : launch_decode<4, 128, false, false, false, 4>(g, st);
+  return bf16 ? launch_decode<4, 128, true, false, false, 32>(g, st) : launch_decode<4, 128, false, false, false, 32>(g, st);
 }
 
 }  // namespace ts
