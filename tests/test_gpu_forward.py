@@ -141,6 +141,32 @@ def test_cfg4_prefill_2048(bits):
     assert err <= TOL
 
 
+# the 70B layer's adaptive mix (attention 8-bit, MLP 4-bit,
+# down 2-bit companded), fp16 N(0, 0.015) weights with outliers.
+CFG5_OPTS = {
+    "q": dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True),
+    "k": dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True),
+    "v": dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True),
+    "o": dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True),
+    "gate": NF4, "up": NF4,
+    "down": dict(bits=2, group_size=64, outlier_frac=0.001, double_quant=True, companded=True),
+}
+
+
+@pytest.mark.slow
+def test_cfg5_llama70b_layer_decode():
+    torch.manual_seed(7)
+    for i, (name, n, k) in enumerate(recipes.LLAMA3_70B_LINEARS):
+        ql, W = _layer(n, k, 5100 + i, CFG5_OPTS[name], sigma=0.015)
+        for M in (1, 4, 16):
+            x = recipes.activations(M, k, seed=M).cuda()
+            err = max_rel_err(ql(x).float(), x.float() @ W.T)
+            say("cfg5", name, M, err)
+            assert err <= TOL, (name, M, err)
+        del ql, W
+        torch.cuda.empty_cache()
+
+
 def test_kernel_api_functions():
     ts = _ts()
     spec, res, d, w = load_case("u4_dq_g128_bias")
