@@ -22,6 +22,8 @@ Alongside it (extra keys of the same JSON line):
   * "roofline"     - the decode kernel: algorithmic bytes of a step's launches /
                      the sum of their average durations (HIP events around
                      graph replays of each launch over the copies), vs 8 TB/s;
+  * "decode_cfg5"  - the same decode step on BASELINE config 5's 70B layer
+                     (its 8/4/2-bit mix), 3 rotating copies (1.4 GB);
   * "prefill"      - BASELINE config 4: gate/up/down at M=2048, 8-bit NF8 + DQ
                      and 6-bit RVQ, 2*M*N*K flops / kernel time vs 2.5 PFLOP/s;
   * "quantize"     - BASELINE config 5's GPU GOAP quantize (28672x8192) through
@@ -84,19 +86,32 @@ def clone_layer(ql):
     return c
 
 
-def build_decode_layer(opts):
+def build_decode_layer(linears, opts_of, sigma=0.02, seed0=1000):
+    """Quantized QuantLinears of one decoder layer: (name, out, in) shapes,
+    per-linear quantize options, seeded N(0, sigma) weights with outliers."""
     import recipes
     import tensorshrink_amd as ts
     layer = []
-    for i, (name, n, k) in enumerate(recipes.LLAMA3_8B_LINEARS):
-        w = recipes.gaussian_weight(n, k, recipes.layer_seed(i))
+    for i, (name, n, k) in enumerate(linears):
+        w = recipes.gaussian_weight(n, k, seed0 + i, sigma=sigma)
         t0 = time.time()
-        qt = ts.quantize_tensor(w, **opts)
+        qt = ts.quantize_tensor(w, **opts_of(name))
         ql = ts.QuantLinear(qt)
         log(f"  quantized {name} {n}x{k} in {time.time() - t0:.2f}s")
         layer.append((name, ql))
+        del w
     return layer
 
+
+# BASELINE config 5: the 70B layer's adaptive mix (attention 8-bit, MLP 4-bit,
+# down 2-bit companded).
+CFG5_OPTS = {
+    **{n: dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+       for n in ("q", "k", "v", "o")},
+    **{n: dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+       for n in ("gate", "up")},
+    "down": dict(bits=2, group_size=64, outlier_frac=0.001, double_quant=True, companded=True),
+}
 
 # Launches of one decode step: (name, positions in LLAMA3_8B_LINEARS).
 GROUPED_UNITS = [("qkv", (0, 1, 2)), ("o", (3,)), ("gate_up", (4, 5)), ("down", (6,))]
@@ -123,17 +138,18 @@ def run_unit(layer, idx, xs, live=None):
     return ys
 
 
-def bench_decode(args, opts):
+def bench_decode(args, linears, opts_of, n_copies, steps, warmup, kernel_reps, sigma=0.02, seed0=1000):
     import recipes
     torch.cuda.synchronize()
-    base = build_decode_layer(opts)
-    copies = [base] + [[(n, clone_layer(q)) for n, q in base] for _ in range(args.copies - 1)]
-    xs = {4096: recipes.activations(1, 4096).cuda(), 14336: recipes.activations(1, 14336).cuda()}
+    base = build_decode_layer(linears, opts_of, sigma, seed0)
+    copies = [base] + [[(n, clone_layer(q)) for n, q in base] for _ in range(n_copies - 1)]
+    widths = sorted({k for _, _, k in linears})
+    xs = {k: recipes.activations(1, k).cuda() for k in widths}
     step_bytes = sum(layer_bytes(q, 1) for _, q in base)
     units = SINGLE_UNITS if args.ungrouped else GROUPED_UNITS
     stream = torch.cuda.Stream()
     C = len(copies)
-    full, rem = divmod(args.steps, C)
+    full, rem = divmod(steps, C)
     outs = []
     with torch.cuda.stream(stream):
         for layer in copies:  # warm every kernel instantiation outside capture
@@ -151,7 +167,7 @@ def bench_decode(args, opts):
         g_all = capture(C)
         g_rem = capture(rem) if rem else None
         torch.cuda.synchronize()
-        for _ in range(max(1, -(-args.warmup // C))):
+        for _ in range(max(1, -(-warmup // C))):
             g_all.replay()
         torch.cuda.synchronize()
         # timed region: exactly K steps, as K // C replays of the C-step graph
@@ -168,10 +184,10 @@ def bench_decode(args, opts):
             e1.record(stream)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    ms_per_step = (t1 - t0) * 1e3 / steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    step_gpu_ms = sum(a.elapsed_time(b) for a, b, _ in evs) / args.steps
-    kern = unit_kernel_time(copies, xs, stream, units, reps=args.kernel_reps)
+    step_gpu_ms = sum(a.elapsed_time(b) for a, b, _ in evs) / steps
+    kern = unit_kernel_time(copies, xs, stream, units, reps=kernel_reps)
     return dict(ms_per_step=ms_per_step, value=value, step_bytes=step_bytes, kern=kern,
                 base=base, xs=xs, step_gpu_us=step_gpu_ms * 1e3, units=units)
 
@@ -390,6 +406,7 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=10)
     ap.add_argument("--ungrouped", action="store_true", help="one launch per linear (7 per step)")
     ap.add_argument("--no-quantize", action="store_true")
+    ap.add_argument("--no-decode70b", action="store_true")
     ap.add_argument("--quantize-reps", type=int, default=3)
     ap.add_argument("--copy-calib", action="store_true", help="only run the plain-copy PMC calibration")
     args = ap.parse_args()
@@ -402,15 +419,32 @@ def main():
     if args.copy_calib:
         copy_calibration()
         return
+    import recipes
     opts = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
     log("decode: building layers")
-    dec = bench_decode(args, opts)
+    dec = bench_decode(args, recipes.LLAMA3_8B_LINEARS, lambda name: opts, args.copies, args.steps, args.warmup,
+                       args.kernel_reps)
     kern = dec["kern"]
     k_us = sum(v["us"] for v in kern.values())
     achieved = dec["step_bytes"] / (dec["step_gpu_us"] * 1e-6) / 1e9
     log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s; GPU {dec['step_gpu_us']:.1f} "
         f"us/step -> {achieved:.0f} GB/s; isolated launches (resident x) {k_us:.1f} us/layer")
     traffic = load_traffic(dec["units"])
+    d70 = None
+    if not args.no_decode70b:
+        log("decode 70B (config 5): building layers")
+        d70r = bench_decode(args, recipes.LLAMA3_70B_LINEARS, lambda name: CFG5_OPTS[name], 3, 15, 3, 3,
+                            sigma=0.015, seed0=5100)
+        d70 = {"workload": "decode M=1, Llama-3-70B-shaped layer, BASELINE config 5 mix: q/k/v/o 8-bit NF8 + DQ, "
+                           "gate/up 4-bit NF4 + DQ (group 128), down 2-bit companded + DQ (group 64); 3 rotating "
+                           "copies; 4 launches per step",
+               "bytes_per_step": d70r["step_bytes"], "us_per_step": round(d70r["ms_per_step"] * 1e3, 2),
+               "GBps": round(d70r["value"], 1), "frac_of_hbm_peak": round(d70r["value"] / HBM_PEAK_GBS, 4),
+               "step_gpu_us": round(d70r["step_gpu_us"], 2),
+               "per_launch_isolated": d70r["kern"]}
+        log(f"decode 70B: {d70['us_per_step']} us/step, {d70['GBps']} GB/s")
+        del d70r
+        torch.cuda.empty_cache()
     pre = None
     if not args.no_prefill:
         log("prefill: M=2048")
@@ -455,6 +489,7 @@ def main():
                      "isolated_launch_us_per_layer": round(k_us, 2),
                      "per_launch_isolated": kern,
                      "traffic_per_launch": traffic["per_launch_bytes"] if traffic else None},
+        "decode_cfg5": d70,
         "prefill": pre,
         "quantize": quant,
         "cpu_baseline": cpu,

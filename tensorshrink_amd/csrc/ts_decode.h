@@ -92,11 +92,11 @@ struct DecodeGroup {
   int n;
 };
 
-constexpr size_t DEC_XLDS_MAX = 32 * 1024;  // activations staged in LDS up to this size
+constexpr size_t DEC_XLDS_MAX = 64 * 1024;  // activations staged in LDS up to this size
 enum { XM_GLOBAL = 0, XM_DMA = 1, XM_REG = 2 };
-// 16-byte x chunks per thread with XM_REG: 4 with 8 waves (x up to 32 KB,
-// a 14336-wide row at M = 1), else 2.
-constexpr int xreg_chunks(int w) { return w == 8 ? 4 : 2; }
+// 16-byte x chunks per thread with XM_REG: 4 with 8 or 16 waves (x up to
+// 32 / 64 KB: a 14336- / 28672-wide row at M = 1), else 2.
+constexpr int xreg_chunks(int w) { return w >= 8 ? 4 : 2; }
 
 template <bool BF16>
 TS_DEV uint32_t pack2(float lo, float hi) {
