@@ -177,6 +177,15 @@ def _gpu_weight(w2d: torch.Tensor, dev) -> torch.Tensor:
     return t.to(dev).contiguous()
 
 
+def _to_host(t: torch.Tensor) -> np.ndarray:
+    """Device tensor -> numpy through page-locked memory from torch's caching
+    host allocator (a DMA at full link rate instead of a staged pageable copy).
+    The array keeps the page-locked block alive; freed blocks are reused."""
+    h = torch.empty(t.shape, dtype=t.dtype, pin_memory=True)
+    h.copy_(t)
+    return h.numpy()
+
+
 def _topk_outliers(wg: torch.Tensor, k: int) -> Tuple[np.ndarray, np.ndarray]:
     """(indices, |w| values) of torch.topk(|w|, k) in CPU order (codec.py:533-535)."""
     lib = L.lib()
@@ -193,8 +202,8 @@ def _topk_outliers(wg: torch.Tensor, k: int) -> Tuple[np.ndarray, np.ndarray]:
         cval = torch.empty(nc, dtype=torch.float32, device=wg.device)
         L.check(lib.ts_topk_candidates_write(ctypes.byref(qi), k, ws.data_ptr(), cidx.data_ptr(), cval.data_ptr(),
                                              st), "topk candidates")
-        ci = cidx.cpu().numpy()
-        cv = cval.cpu().numpy()
+        ci = _to_host(cidx)
+        cv = _to_host(cval)
     else:
         # nth_element regime (k > n / 64): the selection needs every element.
         cv = wg.reshape(-1).to(torch.float32).abs().cpu().numpy()
@@ -228,7 +237,7 @@ def _quantize_2d(wg: torch.Tensor, rows: int, cols: int, bits: int, group_size: 
         L.check(lib.ts_gather_f16(wg.data_ptr(), L.dtype_code(wg.dtype), idx_dev.data_ptr(), k, oval.data_ptr(), st),
                 "outlier values")
         outlier_idx = oi.astype(np.int32)
-        outlier_val = oval.cpu().numpy()
+        outlier_val = _to_host(oval)
         clamp = 1
     else:
         outlier_idx = np.zeros(0, np.int32)
@@ -288,13 +297,13 @@ def _quantize_2d(wg: torch.Tensor, rows: int, cols: int, bits: int, group_size: 
             recon = torch.empty_like(v)
             L.check(lib.ts_double_quantize(v.data_ptr(), nsg, dq_group_size, codes.data_ptr(), meta.data_ptr(),
                                            recon.data_ptr(), st), "double quant")
-            res[f"dq_{name}_codes"] = codes.cpu().numpy()
-            res[f"dq_{name}_meta"] = meta.cpu().numpy()
-            res[name] = recon.cpu().numpy()
+            res[f"dq_{name}_codes"] = _to_host(codes)
+            res[f"dq_{name}_meta"] = _to_host(meta)
+            res[name] = _to_host(recon)
     else:
-        res["scale"] = s16.cpu().numpy()
-        res["gmin"] = g16.cpu().numpy()
-    res["packed"] = packed.cpu().numpy()
+        res["scale"] = _to_host(s16)
+        res["gmin"] = _to_host(g16)
+    res["packed"] = _to_host(packed)
     return res
 
 

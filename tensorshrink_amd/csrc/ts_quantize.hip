@@ -156,8 +156,9 @@ __global__ __launch_bounds__(256) void topk_thr_kernel(const uint32_t* hist, int
 
 TS_DEV bool is_candidate(const void* w, int dt, int64_t i, int64_t k, const uint32_t* thr, int s0, int64_t e0) {
   if (i < k) return true;
-  const uint32_t a = abs_bits(w, dt, i);
-  return __builtin_bit_cast(float, a) > __builtin_bit_cast(float, thr[seg_in_chunk(i, s0, e0, k)]);
+  // Bit patterns of non-negative floats order as the values do, and NaN
+  // patterns lie above +inf: NaN, which the selection ranks first, stays in.
+  return abs_bits(w, dt, i) > thr[seg_in_chunk(i, s0, e0, k)];
 }
 
 __global__ __launch_bounds__(256) void topk_count_kernel(const void* w, int dt, int64_t n, int64_t k,
@@ -269,10 +270,94 @@ static bool topk_cmp(const elem_t& x, const elem_t& y) {
   return (std::isnan(x.first) && !std::isnan(y.first)) || (x.first > y.first);
 }
 
+// The same heap steps as libstdc++'s __heap_select / __adjust_heap /
+// __push_heap / __sort_heap (the steps std::partial_sort runs, and with them
+// torch.topk on the CPU), on one 64-bit word per entry: the value's float
+// bits above a 32-bit index. A level of the sift is then one 16-byte sibling
+// pair, a float compare and a select (no branch to mispredict), with the
+// grandchildren prefetched. Valid when no value is NaN (the comparator is
+// then `a > b`) and every index fits 32 bits; every move, tie and order is
+// that of the std:: calls.
+struct PackedHeap {
+  uint64_t* h;
+  static inline float val(uint64_t e) { return __builtin_bit_cast(float, (uint32_t)(e >> 32)); }
+  // __adjust_heap(first, hole, len, x) followed by __push_heap.
+  inline void adjust(int64_t hole, int64_t len, uint64_t x) {
+    const int64_t top = hole;
+    int64_t child = hole;
+    while (child < (len - 1) / 2) {
+      child = 2 * (child + 1);
+      const uint64_t r = h[child], l = h[child - 1];
+      const bool left = val(r) > val(l);  // comp(first[child], first[child - 1]), comp = greater
+      child -= left;
+      h[hole] = left ? l : r;
+      hole = child;
+      __builtin_prefetch(h + 4 * hole + 3);
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+      child = 2 * (child + 1);
+      h[hole] = h[child - 1];
+      hole = child - 1;
+    }
+    const float xv = val(x);
+    int64_t parent = (hole - 1) / 2;
+    while (hole > top && val(h[parent]) > xv) {  // comp(first[parent], value)
+      h[hole] = h[parent];
+      hole = parent;
+      parent = (hole - 1) / 2;
+    }
+    h[hole] = x;
+  }
+};
+
+static void topk_heap_packed(const int64_t* cidx, const float* cval, int64_t nc, int64_t k, int64_t* out_idx,
+                             float* out_val) {
+  auto pack = [](float v, int64_t i) { return (uint64_t)__builtin_bit_cast(uint32_t, v) << 32 | (uint32_t)i; };
+  std::vector<uint64_t> buf((size_t)k);
+  PackedHeap H{buf.data()};
+  uint64_t* h = H.h;
+  for (int64_t j = 0; j < k; ++j) h[j] = pack(cval[j], cidx[j]);
+  // __make_heap
+  if (k >= 2) {
+    for (int64_t parent = (k - 2) / 2;; --parent) {
+      H.adjust(parent, k, h[parent]);
+      if (parent == 0) break;
+    }
+  }
+  // __heap_select: an element beating the top (comp(e, first): e > top)
+  // replaces it through __pop_heap(first, middle, e) = __adjust_heap(first, 0, k, e)
+  float topv = PackedHeap::val(h[0]);
+  for (int64_t j = k; j < nc; ++j) {
+    const float e = cval[j];
+    if (e > topv) {
+      H.adjust(0, k, pack(e, cidx[j]));
+      topv = PackedHeap::val(h[0]);
+    }
+  }
+  // __sort_heap: repeatedly __pop_heap(first, last - 1, last - 1)
+  for (int64_t last = k; last > 1; --last) {
+    const uint64_t x = h[last - 1];
+    h[last - 1] = h[0];
+    H.adjust(0, last - 1, x);
+  }
+  for (int64_t j = 0; j < k; ++j) {
+    out_idx[j] = (int64_t)(uint32_t)h[j];
+    out_val[j] = PackedHeap::val(h[j]);
+  }
+}
+
 int topk_select(const int64_t* cidx, const float* cval, int64_t nc, int64_t n, int64_t k, int64_t* out_idx,
                 float* out_val) {
   if (k <= 0 || k > n || nc < k) return TS_BAD_ARG;
   if (k * 64 <= n) {
+    for (int64_t i = 0; i < k; ++i)
+      if (cidx[i] != i) return TS_BAD_ARG;  // the stream must start with [0, k)
+    bool packable = n <= (int64_t)UINT32_MAX + 1;
+    for (int64_t j = 0; j < nc && packable; ++j) packable = !std::isnan(cval[j]);
+    if (packable) {
+      topk_heap_packed(cidx, cval, nc, k, out_idx, out_val);
+      return TS_OK;
+    }
     // __heap_select: make_heap(first k); for later elements beating the top,
     // __pop_heap(first, middle, it) == write it at slot k, pop_heap over k+1.
     std::vector<elem_t> h((size_t)k + 1);

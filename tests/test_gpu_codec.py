@@ -114,3 +114,19 @@ def test_config_scale_digests(name):
         ql = ts.QuantLinear(qt)
         for f, h in dig["ql_digests"].items():
             assert sha(getattr(ql, f).cpu().numpy()) == h, f
+
+
+@pytest.mark.parametrize("dtype,k", [(torch.float16, 2000), (torch.float32, 2000), (torch.float16, 2)])
+def test_topk_outliers_with_nan(dtype, k):
+    """NaN weights rank above every number in torch.topk; the device candidate
+    filter keeps them and the host replay puts them where torch does."""
+    from oracle import codec_ref as O
+    from tensorshrink_amd import codec
+    g = torch.Generator().manual_seed(k)
+    w = torch.randn(512, 4096, generator=g).to(dtype)
+    w.view(-1)[[5, 70000, 1500000, 2000000]] = float("nan")
+    say("topk nan", dtype, k)
+    oi, ov = codec._topk_outliers(w.cuda(), k)
+    ov_ref, oi_ref = O.topk_abs(w.float().reshape(-1).numpy(), k)
+    np.testing.assert_array_equal(oi, oi_ref)
+    np.testing.assert_array_equal(ov, ov_ref)

@@ -50,7 +50,7 @@ def _select(lib, cidx, cval, n, k):
 def _prefix_filter(a, k):
     """The GPU candidate rule restated on the CPU: [0, k) plus, in segment
     [k 2^(s-1), k 2^s), values above a lower bound of the k-th largest of the
-    preceding prefix (here: that exact value, the tightest valid bound)."""
+    preceding prefix (here: that exact value, the tightest valid bound), and NaN."""
     n = a.shape[0]
     keep = np.zeros(n, bool)
     keep[:k] = True
@@ -58,13 +58,13 @@ def _prefix_filter(a, k):
     while start < n:
         end = min(2 * start, n)
         kth = np.partition(a[:start], start - k)[start - k]
-        keep[start:end] = a[start:end] > kth
+        keep[start:end] = (a[start:end] > kth) | np.isnan(a[start:end])
         start = end
     return keep
 
 
 @pytest.mark.parametrize("n,k,kind", [(200000, 200, "gauss"), (120000, 1500, "ties"), (65536, 1024, "ties"),
-                                      (5000, 600, "ties"), (5000, 4999, "gauss")])
+                                      (5000, 600, "ties"), (5000, 4999, "gauss"), (100000, 300, "nan")])
 def test_topk_select_replay(n, k, kind):
     L, lib = _lib()
     g = torch.Generator().manual_seed(n ^ k)
@@ -72,7 +72,11 @@ def test_topk_select_replay(n, k, kind):
         a = (torch.randint(-30, 31, (n,), generator=g).float() / 30).to(torch.float16).float().abs().numpy()
     else:
         a = torch.randn(n, generator=g).to(torch.float16).float().abs().numpy()
+    if kind == "nan":  # NaN ranks above every number (the std:: path)
+        a[[7, 5000, 77777]] = np.nan
     ov_ref, oi_ref = O.topk_abs(a, k)
+    tv, ti = torch.topk(torch.from_numpy(a), k)
+    np.testing.assert_array_equal(oi_ref, ti.numpy())
     rc, oi, ov = _select(lib, np.arange(n), a, n, k)
     assert rc == 0
     np.testing.assert_array_equal(oi, oi_ref)
