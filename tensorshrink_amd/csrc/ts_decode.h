@@ -93,10 +93,41 @@ struct DecodeGroup {
 };
 
 constexpr size_t DEC_XLDS_MAX = 64 * 1024;  // activations staged in LDS up to this size
-enum { XM_GLOBAL = 0, XM_DMA = 1, XM_REG = 2 };
+enum { XM_GLOBAL = 0, XM_DMA = 1, XM_REG = 2, XM_DPP = 3 };
 // 16-byte x chunks per thread with XM_REG: 4 with 8 or 16 waves (x up to
 // 32 / 64 KB: a 14336- / 28672-wide row at M = 1), else 2.
 constexpr int xreg_chunks(int w) { return w >= 8 ? 4 : 2; }
+
+// Lane S of each 16-lane row of the wave, to every lane of that row (DPP
+// row_newbcast; S must be a constant once the caller's loops are unrolled).
+template <int S>
+TS_DEV uint32_t dpp_row_bcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + S, 0xf, 0xf, true);
+}
+template <int S>
+TS_DEV ts_u32x4 row_bcast4(ts_u32x4 v) {
+  return ts_u32x4{dpp_row_bcast<S>(v.x), dpp_row_bcast<S>(v.y), dpp_row_bcast<S>(v.z), dpp_row_bcast<S>(v.w)};
+}
+TS_DEV ts_u32x4 row_bcast(ts_u32x4 v, int s) {
+  switch (s) {
+    case 0: return row_bcast4<0>(v);
+    case 1: return row_bcast4<1>(v);
+    case 2: return row_bcast4<2>(v);
+    case 3: return row_bcast4<3>(v);
+    case 4: return row_bcast4<4>(v);
+    case 5: return row_bcast4<5>(v);
+    case 6: return row_bcast4<6>(v);
+    case 7: return row_bcast4<7>(v);
+    case 8: return row_bcast4<8>(v);
+    case 9: return row_bcast4<9>(v);
+    case 10: return row_bcast4<10>(v);
+    case 11: return row_bcast4<11>(v);
+    case 12: return row_bcast4<12>(v);
+    case 13: return row_bcast4<13>(v);
+    case 14: return row_bcast4<14>(v);
+    default: return row_bcast4<15>(v);
+  }
+}
 
 template <bool BF16>
 TS_DEV uint32_t pack2(float lo, float hi) {
@@ -165,7 +196,12 @@ struct DecGeom {
 // with direct global->LDS loads. XM_REG keeps the compiler's wait counts
 // exact, so a wave computes its first batch while the second is in flight;
 // with direct-to-LDS loads pending the compiler treats the load counter as
-// out of order and its first wait drains everything.
+// out of order and its first wait drains everything. XM_DPP (M = 1): no LDS
+// staging; each batch brings its x columns in one 16-byte load per lane, lane
+// 16 q + s holding the chunk that MFMA (u, j) = (s / NMF, s % NMF) of lane
+// group q needs, and a DPP row broadcast of lane s hands it to all 16 lanes of
+// row q. This takes the x operand off the LDS, which the code-table lookups
+// already keep busy.
 // AL: the row's group count is a multiple of U, so every batch starts on a
 // multiple of U in the row-major (row, group) metadata arrays and its U codes
 // / scales come in one aligned vector load.
@@ -176,7 +212,7 @@ template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) {
   constexpr int NT = 64 * W;
   constexpr int R = dec_rep(REP, W);  // table copies
-  constexpr bool XLDS = XM != XM_GLOBAL;
+  constexpr bool XLDS = XM != XM_GLOBAL && XM != XM_DPP;
   extern __shared__ __align__(16) unsigned char smem[];
   using Geo = DecGeom<BITS, GS, RVQ>;
   constexpr int GB = Geo::GB, LB = Geo::LB, GB2 = Geo::GB2, LB2 = Geo::LB2;
@@ -258,6 +294,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     int split;                      // groups u < split use the first super-group
     uint32_t s2s[RVQ ? (AL ? NW16 : U) : 1], s2g[RVQ ? (AL ? NW16 : U) : 1];  // RVQ stage-2 f16 bits
     uint32_t live;                  // bit u set when group u of the batch exists
+    ts_u32x4 xv;                    // XM_DPP: this lane's x chunk of the batch
   };
 
   auto load_batch = [&](int64_t tile, int b, Batch& B) {
@@ -268,6 +305,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     const int64_t r = any ? min(tile * 16 + n, a.N - 1) : min(tile * 16, a.N - 1);
     const uint8_t* wp = a.packed + r * a.pstride + (any ? q * LB : 0);
     const int gb0 = any ? gb : g_lo;  // a dead batch re-reads the wave's first groups
+    if constexpr (XM == XM_DPP) {
+      // chunk of group gb0 + s / NMF, columns (NMF q + s % NMF) * 8 .. + 8 of it
+      const int sl = lane & 15;
+      const int col = (gb0 + sl / NMF) * GS + (NMF * q + sl % NMF) * 8;
+      const ts_u32x4 v = ts_ld16(a.x + min(col, (int)a.cols - 8));
+      B.xv = (sl < U * NMF && col < a.cols) ? v : ts_u32x4{0u, 0u, 0u, 0u};
+    }
     int gg[U];
     B.live = 0;
 #pragma unroll
@@ -357,7 +401,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
         // A-operand row n >= M only feeds output rows that are never stored,
         // so those lanes read row M - 1 (no predicate, one base per lane).
         if constexpr (CPM == 8) {
-          if constexpr (XLDS) {
+          if constexpr (XM == XM_DPP) {
+            xa[j] = row_bcast(B.xv, u * NMF + j);
+          } else if constexpr (XLDS) {
             xa[j] = *reinterpret_cast<const ts_u32x4*>(xrow_lds + col);
           } else {
             const ts_u32x4 v = ts_ld16(xrow_glb + min(col, (int)a.cols - 8));
@@ -729,11 +775,23 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   const DecShape sh = decode_shape(g.tile_end[g.n - 1], a.n_groups, UMAX);
   // x through registers when xreg_chunks(w) chunks per thread hold it
   auto xreg = [&](int w) { return xlds && (int64_t)a.M * a.K / 8 <= (int64_t)xreg_chunks(w) * 64 * w; };
+  // M = 1: x through DPP row broadcasts when a batch's (group, MFMA) pairs fit
+  // the 16 lanes of a row
+  constexpr bool DPP_OK = !(BITS == 8 && CB8) && UMAX * (GS / 32) <= 16;
+  const bool dpp = DPP_OK && a.M == 1;
 #define TS_DEC(XMV, DQV, ALV, WV, UV, LP) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, LP>(g, st)
 #define TS_DEC_ALL(DQV)                                                          \
   do {                                                                           \
     const bool alm = aligned(UMAX);                                              \
+    if constexpr (DPP_OK) {                                                      \
+      if (dpp && sh.ok && alm) {                                                 \
+        if (sh.W == 4) TS_DEC(XM_DPP, DQV, true, 4, UMAX, false);                \
+        if (sh.W == 8) TS_DEC(XM_DPP, DQV, true, 8, UMAX, false);                \
+        TS_DEC(XM_DPP, DQV, true, 16, UMAX, false);                              \
+      }                                                                          \
+      if (dpp && alm) TS_DEC(XM_DPP, DQV, true, 16, UMAX, true);                 \
+    }                                                                            \
     if (xlds && sh.ok && alm) {                                                  \
       if (sh.W == 4) {                                                           \
         if (xreg(4)) TS_DEC(XM_REG, DQV, true, 4, UMAX, false);                  \
