@@ -105,27 +105,32 @@ TS_DEV uint32_t dpp_row_bcast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + S, 0xf, 0xf, true);
 }
 template <int S>
-TS_DEV ts_u32x4 row_bcast4(ts_u32x4 v) {
+TS_DEV ts_u32x4 row_bcast_(ts_u32x4 v) {
   return ts_u32x4{dpp_row_bcast<S>(v.x), dpp_row_bcast<S>(v.y), dpp_row_bcast<S>(v.z), dpp_row_bcast<S>(v.w)};
 }
-TS_DEV ts_u32x4 row_bcast(ts_u32x4 v, int s) {
+template <int S>
+TS_DEV ts_u32x2 row_bcast_(ts_u32x2 v) {
+  return ts_u32x2{dpp_row_bcast<S>(v.x), dpp_row_bcast<S>(v.y)};
+}
+template <typename V>
+TS_DEV V row_bcast(V v, int s) {
   switch (s) {
-    case 0: return row_bcast4<0>(v);
-    case 1: return row_bcast4<1>(v);
-    case 2: return row_bcast4<2>(v);
-    case 3: return row_bcast4<3>(v);
-    case 4: return row_bcast4<4>(v);
-    case 5: return row_bcast4<5>(v);
-    case 6: return row_bcast4<6>(v);
-    case 7: return row_bcast4<7>(v);
-    case 8: return row_bcast4<8>(v);
-    case 9: return row_bcast4<9>(v);
-    case 10: return row_bcast4<10>(v);
-    case 11: return row_bcast4<11>(v);
-    case 12: return row_bcast4<12>(v);
-    case 13: return row_bcast4<13>(v);
-    case 14: return row_bcast4<14>(v);
-    default: return row_bcast4<15>(v);
+    case 0: return row_bcast_<0>(v);
+    case 1: return row_bcast_<1>(v);
+    case 2: return row_bcast_<2>(v);
+    case 3: return row_bcast_<3>(v);
+    case 4: return row_bcast_<4>(v);
+    case 5: return row_bcast_<5>(v);
+    case 6: return row_bcast_<6>(v);
+    case 7: return row_bcast_<7>(v);
+    case 8: return row_bcast_<8>(v);
+    case 9: return row_bcast_<9>(v);
+    case 10: return row_bcast_<10>(v);
+    case 11: return row_bcast_<11>(v);
+    case 12: return row_bcast_<12>(v);
+    case 13: return row_bcast_<13>(v);
+    case 14: return row_bcast_<14>(v);
+    default: return row_bcast_<15>(v);
   }
 }
 
@@ -197,10 +202,10 @@ struct DecGeom {
 // exact, so a wave computes its first batch while the second is in flight;
 // with direct-to-LDS loads pending the compiler treats the load counter as
 // out of order and its first wait drains everything. XM_DPP (M = 1): no LDS
-// staging; each batch brings its x columns in one 16-byte load per lane, lane
-// 16 q + s holding the chunk that MFMA (u, j) = (s / NMF, s % NMF) of lane
-// group q needs, and a DPP row broadcast of lane s hands it to all 16 lanes of
-// row q. This takes the x operand off the LDS, which the code-table lookups
+// staging; each batch brings its x columns in one load per lane (CPM
+// columns), lane 16 q + s holding the chunk that MFMA (u, j) = (s / NMF,
+// s % NMF) of lane group q needs, and a DPP row broadcast of lane s hands it
+// to all 16 lanes of row q. This takes the x operand off the LDS, which the code-table lookups
 // already keep busy.
 // AL: the row's group count is a multiple of U, so every batch starts on a
 // multiple of U in the row-major (row, group) metadata arrays and its U codes
@@ -306,11 +311,17 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     const uint8_t* wp = a.packed + r * a.pstride + (any ? q * LB : 0);
     const int gb0 = any ? gb : g_lo;  // a dead batch re-reads the wave's first groups
     if constexpr (XM == XM_DPP) {
-      // chunk of group gb0 + s / NMF, columns (NMF q + s % NMF) * 8 .. + 8 of it
+      // chunk of group gb0 + s / NMF, columns (NMF q + s % NMF) * CPM .. + CPM of it
       const int sl = lane & 15;
-      const int col = (gb0 + sl / NMF) * GS + (NMF * q + sl % NMF) * 8;
-      const ts_u32x4 v = ts_ld16(a.x + min(col, (int)a.cols - 8));
-      B.xv = (sl < U * NMF && col < a.cols) ? v : ts_u32x4{0u, 0u, 0u, 0u};
+      const int col = (gb0 + sl / NMF) * GS + (NMF * q + sl % NMF) * CPM;
+      const bool use = sl < U * NMF && col < a.cols;
+      if constexpr (CPM == 8) {
+        const ts_u32x4 v = ts_ld16(a.x + min(col, (int)a.cols - 8));
+        B.xv = use ? v : ts_u32x4{0u, 0u, 0u, 0u};
+      } else {
+        const ts_u32x2 v = ts_ld8(a.x + min(col, (int)a.cols - 4));
+        B.xv = use ? ts_u32x4{v.x, v.y, 0u, 0u} : ts_u32x4{0u, 0u, 0u, 0u};
+      }
     }
     int gg[U];
     B.live = 0;
@@ -411,7 +422,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
           }
         } else {
           ts_u32x2 v;
-          if constexpr (XLDS) {
+          if constexpr (XM == XM_DPP) {
+            v = row_bcast(ts_u32x2{B.xv.x, B.xv.y}, u * NMF + j);
+          } else if constexpr (XLDS) {
             v = *reinterpret_cast<const ts_u32x2*>(xrow_lds + col);
           } else {
             const ts_u32x2 l = ts_ld8(xrow_glb + min(col, (int)a.cols - 4));
@@ -777,7 +790,7 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   auto xreg = [&](int w) { return xlds && (int64_t)a.M * a.K / 8 <= (int64_t)xreg_chunks(w) * 64 * w; };
   // M = 1: x through DPP row broadcasts when a batch's (group, MFMA) pairs fit
   // the 16 lanes of a row
-  constexpr bool DPP_OK = !(BITS == 8 && CB8) && UMAX * (GS / 32) <= 16;
+  constexpr bool DPP_OK = UMAX * ((BITS == 8 && CB8) ? GS / 16 : GS / 32) <= 16;
   const bool dpp = DPP_OK && a.M == 1;
 #define TS_DEC(XMV, DQV, ALV, WV, UV, LP) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, LP>(g, st)
