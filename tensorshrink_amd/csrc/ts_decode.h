@@ -190,11 +190,12 @@ struct DecGeom {
 };
 
 // W: waves per workgroup (4, 8 or 16), all on the same tile, each owning a
-// contiguous run of its batches of U groups. Without LOOP every wave has at
-// most two batches and the kernel is straight-line code. The host spreads a
-// tile over more waves (smaller U) when there are few tiles, so a small layer
-// still has several waves per SIMD to hide LDS and MFMA latency. LOOP streams
-// longer runs through the two register buffers.
+// contiguous run of its batches of U groups. NB = 1 or 2: every wave has at
+// most NB batches and the kernel is straight-line code (with NB = 1 no second
+// batch is loaded at all). The host spreads a tile over more waves when there
+// are few tiles, so a small layer still has several waves per SIMD to hide
+// LDS and MFMA latency. NB = 0 (LOOP) streams longer runs through the two
+// register buffers.
 // XM: where the A operand (x) comes from: XM_GLOBAL reads it from global
 // memory per MFMA (x too large for LDS); XM_REG stages it in LDS through
 // registers (at most xreg_chunks(W) 16-byte chunks per thread); XM_DMA stages it
@@ -213,9 +214,10 @@ struct DecGeom {
 // Occupancy: at most 128 VGPRs (4 waves per SIMD, 16 per CU), so 1024 waves
 // of 16-row tiles are resident at once across 256 CUs.
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
-          bool LOOP>
+          int NB>
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) {
   constexpr int NT = 64 * W;
+  constexpr bool LOOP = NB == 0;
   constexpr int R = dec_rep(REP, W);  // table copies
   constexpr bool XLDS = XM != XM_GLOBAL && XM != XM_DPP;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -624,7 +626,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // soon as its own loads land.
   Batch bufA, bufB;
   load_batch(tile, 0, bufA);
-  load_batch(tile, 1, bufB);  // (a dead batch when nb == 1)
+  if constexpr (NB != 1) load_batch(tile, 1, bufB);  // (a dead batch when nb == 1)
   // This tile's outlier slots sit at a fixed address (no dependent load):
   // each thread takes slots tid and tid + NT; more (rare) are read in the
   // epilogue. Indices past cap read a valid slot whose value is dropped.
@@ -648,7 +650,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // the same loads in the same order.
   if constexpr (!LOOP) {
     compute_batch(0, bufA, yacc);
-    if (nb > 1) compute_batch(1, bufB, yacc);
+    if constexpr (NB == 2) {
+      if (nb > 1) compute_batch(1, bufB, yacc);
+    }
   } else {
     for (int b = 0; b < nb; b += 2) {
       compute_batch(b, bufA, yacc);
@@ -717,11 +721,11 @@ inline size_t decode_smem(int M, int64_t K, bool xlds) {
 }
 
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
-          bool LOOP>
+          int NB>
 inline int launch_decode_x(const DecodeGroup& g, hipStream_t st) {
   const DecodeArgs& a = g.a[0];
   const size_t smem = decode_smem<BITS, CB8, RVQ, REP, W>(a.M, a.K, XM != XM_GLOBAL);
-  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, LOOP>;
+  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -792,15 +796,25 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   // the 16 lanes of a row
   constexpr bool DPP_OK = UMAX * ((BITS == 8 && CB8) ? GS / 16 : GS / 32) <= 16;
   const bool dpp = DPP_OK && a.M == 1;
+  const bool one = (a.n_groups + UMAX - 1) / UMAX <= sh.W;  // one batch per wave
 #define TS_DEC(XMV, DQV, ALV, WV, UV, LP) \
-  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, LP>(g, st)
+  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, (LP) ? 0 : 2>(g, st)
+#define TS_DEC1(XMV, DQV, ALV, WV, UV) \
+  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, 1>(g, st)
 #define TS_DEC_ALL(DQV)                                                          \
   do {                                                                           \
     const bool alm = aligned(UMAX);                                              \
     if constexpr (DPP_OK) {                                                      \
       if (dpp && sh.ok && alm) {                                                 \
-        if (sh.W == 4) TS_DEC(XM_DPP, DQV, true, 4, UMAX, false);                \
-        if (sh.W == 8) TS_DEC(XM_DPP, DQV, true, 8, UMAX, false);                \
+        if (sh.W == 4) {                                                         \
+          if (one) TS_DEC1(XM_DPP, DQV, true, 4, UMAX);                          \
+          TS_DEC(XM_DPP, DQV, true, 4, UMAX, false);                             \
+        }                                                                        \
+        if (sh.W == 8) {                                                         \
+          if (one) TS_DEC1(XM_DPP, DQV, true, 8, UMAX);                          \
+          TS_DEC(XM_DPP, DQV, true, 8, UMAX, false);                             \
+        }                                                                        \
+        if (one) TS_DEC1(XM_DPP, DQV, true, 16, UMAX);                           \
         TS_DEC(XM_DPP, DQV, true, 16, UMAX, false);                              \
       }                                                                          \
       if (dpp && alm) TS_DEC(XM_DPP, DQV, true, 16, UMAX, true);                 \
@@ -825,6 +839,7 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   if (dq) TS_DEC_ALL(true);
   TS_DEC_ALL(false);
 #undef TS_DEC_ALL
+#undef TS_DEC1
 #undef TS_DEC
 }
 
