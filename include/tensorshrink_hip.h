@@ -88,17 +88,21 @@ const char* ts_status_str(int status);
 /* Library version string. */
 const char* ts_version(void);
 
-/* Bytes of device workspace the forward entry points need for M activation
- * rows (0 for every shape the kernels cover directly). */
+/* Bytes of device workspace ts_qlinear_forward uses for M activation rows:
+ * 0 up to 16 rows (the decode kernel), else room for the dequantized layer
+ * (rows x cols in the activation dtype) plus the GEMM library's workspace. */
 size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M);
 
 /*
  * y[M, rows] = x[M, cols] @ W^T + outliers (+ bias), fp32 accumulation, stored
  * in y_dtype. Replaces fused_quantized_linear (triton_kernels.py:714-945) and,
  * for large M, the dequantize_weight + outlier scatter + F.linear path
- * (modules.py:896-922): M <= 16 runs the HBM-bound decode kernel, larger M the
- * MFMA prefill kernel. x_dtype is TS_BF16 or TS_F16; bias (may be NULL) has
- * x_dtype. ldx/ldy are row strides in elements.
+ * (modules.py:896-922): M <= 16 runs the HBM-bound decode kernel; M > 16
+ * with a workspace of ts_forward_workspace_bytes(layer, M) bytes dequantizes
+ * the layer into it and runs one hipBLASLt GEMM (bias in its epilogue);
+ * otherwise the fused MFMA prefill kernel. x_dtype is TS_BF16 or TS_F16; bias
+ * (may be NULL) has x_dtype. ldx/ldy are row strides in elements. Calls that
+ * share a workspace must be ordered on one stream.
  */
 int ts_qlinear_forward(const ts_qlayer* layer, const void* x, int64_t M, int64_t ldx, int x_dtype,
                        void* y, int64_t ldy, int y_dtype, const void* bias,

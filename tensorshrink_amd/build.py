@@ -35,6 +35,7 @@ SOURCES = [
     "ts_decode_b8_g64.hip",
     "ts_decode_b8_g128.hip",
     "ts_prefill.hip",
+    "ts_gemm.hip",
     "ts_prefill_b2_g64.hip",
     "ts_prefill_b2_g128.hip",
     "ts_prefill_b2_g256.hip",
@@ -84,7 +85,9 @@ def build(verbose: bool = True) -> str:
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
+           "-L", rocm_lib, "-lhipblaslt", f"-Wl,-rpath,{rocm_lib}"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr[-4000:]}")

@@ -1,6 +1,7 @@
 // extern "C" entry points of libtensorshrink_hip.so (declared in
 // include/tensorshrink_hip.h). Argument checking and dispatch only; the
-// kernels live in ts_decode.hip, ts_prefill.hip, ts_aux.hip, ts_quantize.hip.
+// kernels live in ts_decode.hip, ts_prefill.hip, ts_gemm.hip, ts_aux.hip,
+// ts_quantize.hip.
 #include "ts_common.h"
 
 namespace ts {
@@ -15,6 +16,14 @@ int generic_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ld
                     int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st);
 int dequantize(const ts_qlayer* L, int mode, const int32_t* oidx, const uint16_t* oval, int64_t n_oidx,
                void* w_out, int64_t ldw, int dt, hipStream_t st);
+size_t gemm_ws_bytes(const ts_qlayer* L);
+int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y, int64_t ldy,
+                 int y_dtype, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st);
+// Above the decode sizes the forward dequantizes the layer into the
+// workspace and runs one library GEMM, when the caller provides it (the
+// reference switches to dequantize + F.linear above 64 rows; measured here the
+// GEMM path is faster than the fused MFMA kernel from 17 rows on).
+constexpr int64_t GEMM_MIN_M = 17;
 int outlier_row_ptr(const int32_t* row, int64_t n, int64_t rows, int32_t* row_ptr, hipStream_t st);
 int tile_outlier_max(const int32_t* rp, int64_t rows, int32_t* out, hipStream_t st);
 int build_tile_outliers(const int32_t* rp, const int32_t* orow, const int32_t* ocol, const uint16_t* odelta,
@@ -77,15 +86,12 @@ const char* ts_status_str(int s) {
 const char* ts_version(void) { return "tensorshrink_hip 0.1.0 (gfx950)"; }
 
 size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M) {
-  (void)layer;
-  (void)M;
-  return 0;
+  if (!layer_ok(layer) || M < ts::GEMM_MIN_M) return 0;
+  return ts::gemm_ws_bytes(layer);
 }
 
 int ts_qlinear_forward(const ts_qlayer* L, const void* x, int64_t M, int64_t ldx, int x_dtype, void* y, int64_t ldy,
                        int y_dtype, const void* bias, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (!layer_ok(L) || !x || !y || M < 0) return TS_BAD_ARG;
   if (x_dtype != TS_BF16 && x_dtype != TS_F16) return TS_BAD_ARG;
   if (y_dtype != TS_BF16 && y_dtype != TS_F16 && y_dtype != TS_F32) return TS_BAD_ARG;
@@ -97,7 +103,9 @@ int ts_qlinear_forward(const ts_qlayer* L, const void* x, int64_t M, int64_t ldx
   // The tiled kernels read x in aligned 16-byte chunks.
   const bool aligned = (L->cols % 8 == 0) && (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
   int rc = TS_NOT_COVERED;
-  if (aligned) {
+  if (M >= ts::GEMM_MIN_M && workspace)
+    rc = ts::gemm_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, workspace, workspace_bytes, S(stream));
+  if (rc == TS_NOT_COVERED && aligned) {
     if (M <= 16) rc = ts::decode_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
     else rc = ts::prefill_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
   }

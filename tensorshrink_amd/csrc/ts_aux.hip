@@ -74,6 +74,104 @@ __global__ void dequant_base_kernel(const ts_qlayer L, void* out, int64_t ldw, i
   }
 }
 
+// Pass 1, vectorised: one thread per 32 consecutive columns of a row (inside
+// one group: group sizes are multiples of 32), its codes in one 8/16/32-byte
+// load, scale/gmin once, 16-byte stores. Same float32 operations as
+// base_value / stage2_value, in the same order, so the output is
+// bit-identical.
+constexpr int DQV_COLS = 32;
+
+template <int BITS>
+TS_DEV void load_codes32(const uint8_t* p, uint32_t (&c)[32]) {
+  if constexpr (BITS == 8) {
+    const ts_u32x4 a = ts_ld16(p), b = ts_ld16(p + 16);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 32; ++i) c[i] = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
+  } else if constexpr (BITS == 4) {
+    const ts_u32x4 a = ts_ld16(p);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 32; ++i) c[i] = (w[i >> 3] >> (4 * (i & 7))) & 15u;
+  } else {
+    const ts_u32x2 a = ts_ld8(p);
+    const uint32_t w[2] = {a.x, a.y};
+#pragma unroll
+    for (int i = 0; i < 32; ++i) c[i] = (w[i >> 4] >> (2 * (i & 15))) & 3u;
+  }
+}
+
+// BITS: 2, 4, 8, or 6 (4-bit stage 1 + 2-bit stage 2)
+template <int BITS, int DT>
+__global__ __launch_bounds__(256) void dequant_vec_kernel(const ts_qlayer L, void* out, int64_t ldw, int64_t cpr) {
+#pragma clang fp contract(off)
+  __shared__ float cbs[256];
+  const bool use_cb = L.codebook && BITS != 6;
+  if (use_cb) {
+    for (int i = threadIdx.x; i < (1 << (BITS == 6 ? 4 : BITS)); i += blockDim.x) cbs[i] = L.codebook[i];
+  }
+  __syncthreads();
+  const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (q >= L.rows * cpr) return;
+  const int64_t row = q / cpr;
+  const int64_t col0 = (q - row * cpr) * DQV_COLS;
+  float s, gm;
+  scale_gmin_f32(L, row, col0 / L.group_size, s, gm);
+  constexpr int B1 = BITS == 6 ? 4 : BITS;
+  uint32_t c[32];
+  load_codes32<B1>(L.packed + row * L.packed_stride + col0 * B1 / 8, c);
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float cv = use_cb ? cbs[c[i]] : (float)c[i];
+    v[i] = cv * s + gm;
+  }
+  if constexpr (BITS == 6) {
+    uint32_t c2[32];
+    load_codes32<2>(L.stage2_packed + row * L.stage2_stride + col0 / 4, c2);
+    const int64_t flat = row * L.n_groups + col0 / L.group_size;
+    const float s2 = ts_h2f(L.stage2_scale[flat]), g2 = ts_h2f(L.stage2_gmin[flat]);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = v[i] + ((float)c2[i] * s2 + g2);
+  }
+  const int64_t off = row * ldw + col0;
+  if (col0 + DQV_COLS <= L.cols) {
+    if constexpr (DT == TS_F32) {
+      float* o = reinterpret_cast<float*>(out) + off;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        *reinterpret_cast<ts_f32x4*>(o + 4 * j) = ts_f32x4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+    } else {
+      uint16_t* o = reinterpret_cast<uint16_t*>(out) + off;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t h[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = v[8 * j + 2 * i], b = v[8 * j + 2 * i + 1];
+          h[i] = DT == TS_BF16 ? ((uint32_t)ts_f2bf(a) | ((uint32_t)ts_f2bf(b) << 16))
+                               : ((uint32_t)ts_f2h(a) | ((uint32_t)ts_f2h(b) << 16));
+        }
+        *reinterpret_cast<ts_u32x4*>(o + 8 * j) = ts_u32x4{h[0], h[1], h[2], h[3]};
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      if (col0 + i < L.cols) store_out(out, off + i, DT, v[i]);
+  }
+}
+
+template <int BITS>
+void launch_dequant_vec(const ts_qlayer& L, void* out, int64_t ldw, int dt, hipStream_t st) {
+  const int64_t cpr = ts_cdiv(L.cols, DQV_COLS);
+  const dim3 grid((unsigned)ts_cdiv(L.rows * cpr, 256));
+  if (dt == TS_F32) hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F32>), grid, dim3(256), 0, st, L, out, ldw, cpr);
+  else if (dt == TS_BF16)
+    hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_BF16>), grid, dim3(256), 0, st, L, out, ldw, cpr);
+  else hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F16>), grid, dim3(256), 0, st, L, out, ldw, cpr);
+}
+
 // Pass 2, codec view (codec.py:793-796, 823-846): the outlier position takes
 // f32(outlier_val) (+ RVQ stage 2), then the cast.
 __global__ void dequant_outlier_codec_kernel(const ts_qlayer L, void* out, int64_t ldw, int dt, const int32_t* idx,
@@ -155,8 +253,24 @@ __global__ void outlier_correction_kernel(float* out, int64_t M, int64_t ldo, co
 int dequantize(const ts_qlayer* Lp, int mode, const int32_t* oidx, const uint16_t* oval, int64_t n_oidx,
                void* w_out, int64_t ldw, int dt, hipStream_t st) {
   const ts_qlayer& L = *Lp;
-  dim3 grid((unsigned)std::min<int64_t>(ts_cdiv(L.cols, 256), 64), (unsigned)L.rows);
-  hipLaunchKernelGGL(dequant_base_kernel, grid, dim3(256), 0, st, L, w_out, ldw, dt);
+  // 16-byte stores need 16-byte aligned rows; the 8-column chunks need group
+  // sizes that are multiples of 8 and code rows whose loads stay aligned
+  const int esz = dt == TS_F32 ? 4 : 2;
+  // code loads of 32 columns: 8 (2-bit), 16 (4-bit) or 32 (8-bit) bytes, so
+  // rows and bases 16-byte aligned (8 for the 2-bit stage-2 plane)
+  const bool vec = (ldw * esz) % 16 == 0 && (reinterpret_cast<uintptr_t>(w_out) & 15) == 0 &&
+                   L.group_size % DQV_COLS == 0 && (L.packed_stride % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(L.packed) & 15) == 0 &&
+                   (L.bits != 6 || ((L.stage2_stride % 8) == 0 && (reinterpret_cast<uintptr_t>(L.stage2_packed) & 7) == 0));
+  if (vec) {
+    if (L.bits == 2) launch_dequant_vec<2>(L, w_out, ldw, dt, st);
+    else if (L.bits == 4) launch_dequant_vec<4>(L, w_out, ldw, dt, st);
+    else if (L.bits == 6) launch_dequant_vec<6>(L, w_out, ldw, dt, st);
+    else launch_dequant_vec<8>(L, w_out, ldw, dt, st);
+  } else {
+    dim3 grid((unsigned)std::min<int64_t>(ts_cdiv(L.cols, 256), 64), (unsigned)L.rows);
+    hipLaunchKernelGGL(dequant_base_kernel, grid, dim3(256), 0, st, L, w_out, ldw, dt);
+  }
   TS_CHECK_LAUNCH();
   if (mode == TS_DEQ_CODEC && n_oidx > 0) {
     hipLaunchKernelGGL(dequant_outlier_codec_kernel, dim3((unsigned)ts_cdiv(n_oidx, 256)), dim3(256), 0, st, L,

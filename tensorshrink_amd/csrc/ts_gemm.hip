@@ -1,0 +1,125 @@
+// Prefill through a dense GEMM: the layer dequantized into the caller's
+// workspace in the activation dtype (outliers included, bit-identical to
+// ts_dequantize), then one hipBLASLt matmul with the bias in its epilogue.
+// This is the reference's own path for M > 64 (modules.py:896-922:
+// dequantize_weight + outlier scatter + F.linear); at prefill sizes the
+// library GEMM runs near the matrix cores' rate, so materialising W costs
+// less than dequantizing every weight tile once per M-tile inside a fused
+// kernel.
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "ts_common.h"
+
+namespace ts {
+
+int dequantize(const ts_qlayer* L, int mode, const int32_t* oidx, const uint16_t* oval, int64_t n_oidx,
+               void* w_out, int64_t ldw, int dt, hipStream_t st);
+
+namespace {
+
+constexpr size_t GEMM_LT_WS = 32u << 20;  // hipBLASLt workspace reserved after W
+
+struct Plan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  size_t ws = 0;
+  bool ok = false;
+};
+
+// (device, M, N, K, ldx, ldy, x dtype, y dtype, bias kind)
+using Key = std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t, int, int, int>;
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;
+std::map<Key, Plan> g_plans;
+
+hipDataType hip_type(int dt) { return dt == TS_F32 ? HIP_R_32F : (dt == TS_BF16 ? HIP_R_16BF : HIP_R_16F); }
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+// y[M, N] (row-major, ld ldy) = x[M, K] (ld ldx) @ W[N, K]^T: in column-major
+// terms D[N, M] = op(A) B with A = W as K x N (transposed), B = x as K x M.
+Plan make_plan(hipblasLtHandle_t h, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, int xdt, int ydt,
+               int bias_kind) {
+  Plan p;
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return p;
+  hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
+  hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
+  if (bias_kind) {
+    const hipblasLtEpilogue_t ep = HIPBLASLT_EPILOGUE_BIAS;
+    const hipDataType bt = hip_type(xdt);
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep));
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
+  }
+  if (hipblasLtMatrixLayoutCreate(&p.a, hip_type(xdt), (uint64_t)K, (uint64_t)N, K) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p.b, hip_type(xdt), (uint64_t)K, (uint64_t)M, ldx) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&p.d, hip_type(ydt), (uint64_t)N, (uint64_t)M, ldy) != HIPBLAS_STATUS_SUCCESS)
+    return p;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
+  const uint64_t wsmax = GEMM_LT_WS;
+  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax, sizeof(wsmax));
+  hipblasLtMatmulHeuristicResult_t res[1];
+  int n = 0;
+  const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, 1, res, &n);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (st != HIPBLAS_STATUS_SUCCESS || n < 1 || res[0].state != HIPBLAS_STATUS_SUCCESS ||
+      res[0].workspaceSize > GEMM_LT_WS)
+    return p;
+  p.algo = res[0].algo;
+  p.ws = res[0].workspaceSize;
+  p.ok = true;
+  return p;
+}
+
+}  // namespace
+
+// Workspace of the GEMM path: W in the activation dtype, then hipBLASLt's.
+size_t gemm_ws_bytes(const ts_qlayer* L) { return align256((size_t)L->rows * (size_t)L->cols * 2) + GEMM_LT_WS; }
+
+// TS_NOT_COVERED when hipBLASLt has no algorithm for the shape (the caller
+// then runs the fused kernel).
+int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y, int64_t ldy,
+                 int y_dtype, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (!ws || ws_bytes < gemm_ws_bytes(L)) return TS_NOT_COVERED;
+  // the bias rides in the epilogue when it has D's type (bf16/f16 output)
+  if (bias && y_dtype != x_dtype) return TS_NOT_COVERED;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return TS_HIP_ERROR;
+  const int64_t N = L->rows, K = L->cols;
+  char* wsb = static_cast<char*>(ws);
+  void* W = wsb;
+  void* lt_ws = wsb + align256((size_t)N * (size_t)K * 2);
+  const int rc = dequantize(L, TS_DEQ_QLINEAR, nullptr, nullptr, 0, W, K, x_dtype, st);
+  if (rc != TS_OK) return rc;
+  std::lock_guard<std::mutex> lock(g_mu);
+  auto hit = g_handles.find(dev);
+  if (hit == g_handles.end()) {
+    hipblasLtHandle_t h = nullptr;
+    if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return TS_HIP_ERROR;
+    hit = g_handles.emplace(dev, h).first;
+  }
+  const Key key{dev, M, N, K, ldx, ldy, x_dtype, y_dtype, bias ? 1 : 0};
+  auto pit = g_plans.find(key);
+  if (pit == g_plans.end()) pit = g_plans.emplace(key, make_plan(hit->second, M, N, K, ldx, ldy, x_dtype, y_dtype,
+                                                                 bias ? 1 : 0)).first;
+  Plan& p = pit->second;
+  if (!p.ok) return TS_NOT_COVERED;
+  if (bias) {
+    const void* bp = bias;
+    hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp));
+  }
+  const float alpha = 1.f, beta = 0.f;
+  if (hipblasLtMatmul(hit->second, p.desc, &alpha, W, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.algo, lt_ws, p.ws, st) !=
+      HIPBLAS_STATUS_SUCCESS)
+    return TS_HIP_ERROR;
+  return TS_OK;
+}
+
+}  // namespace ts

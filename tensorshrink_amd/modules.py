@@ -257,10 +257,14 @@ class QuantLinear(nn.Module):
     def _bias_as(self, dtype: torch.dtype) -> Optional[torch.Tensor]:
         if self.bias is None:
             return None
-        b = self._bias_cache.get(dtype)
+        # keyed on the bias tensor and its version: a reassigned or updated
+        # bias is converted again
+        key = (dtype, id(self.bias), self.bias._version)
+        b = self._bias_cache.get(key)
         if b is None:
+            self._bias_cache = {k: v for k, v in self._bias_cache.items() if k[1:] == key[1:]}
             b = self.bias.to(dtype).contiguous()
-            self._bias_cache[dtype] = b
+            self._bias_cache[key] = b
         return b
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -286,9 +290,13 @@ class QuantLinear(nn.Module):
         y = torch.empty(M, self.out_features, dtype=in_dtype, device=x.device)
         b = self._bias_as(in_dtype)
         dt = L.dtype_code(in_dtype)
-        L.check(L.load().ts_qlinear_forward(ctypes.byref(self._layer), x2d.data_ptr(), M, self.in_features, dt,
-                                            y.data_ptr(), self.out_features, dt, L.ptr(b), None, 0,
-                                            L.stream_ptr(x.device)), "qlinear forward")
+        lib = L.load()
+        # large M: room for the dequantized layer + GEMM (0 below the threshold)
+        ws_n = lib.ts_forward_workspace_bytes(ctypes.byref(self._layer), M)
+        ws = torch.empty(ws_n, dtype=torch.uint8, device=x.device) if ws_n else None
+        L.check(lib.ts_qlinear_forward(ctypes.byref(self._layer), x2d.data_ptr(), M, self.in_features, dt,
+                                       y.data_ptr(), self.out_features, dt, L.ptr(b), L.ptr(ws), ws_n,
+                                       L.stream_ptr(x.device)), "qlinear forward")
         return y.reshape(*lead, self.out_features)
 
     @staticmethod

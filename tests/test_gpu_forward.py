@@ -36,6 +36,11 @@ def test_forward_small_cases(name, M):
         y_ref += bias.double()
     err = max_rel_err(y.cpu(), y_ref)
     assert err <= TOL, err
+    if M > 16:  # the fused MFMA kernel, which runs without a workspace
+        if bias is not None:
+            ql.bias = bias.cuda()
+        err = max_rel_err(_forward_no_workspace(ql, x.cuda()).cpu(), y_ref)
+        assert err <= TOL, ("fused", err)
 
 
 @pytest.mark.parametrize("M", [1, 5, 16, 40])
@@ -228,3 +233,39 @@ def test_forward_group_fallbacks():
         ya, yb = ts.QuantLinear.forward_group([a, b], x)
         assert max_rel_err(ya.float(), x.float() @ Wa.T) <= TOL
         assert max_rel_err(yb.float(), x.float() @ Wb.T) <= TOL
+
+
+def _forward_no_workspace(ql, x):
+    """ts_qlinear_forward without a workspace: the fused MFMA prefill kernel."""
+    import ctypes
+    from tensorshrink_amd import _lib as L
+    y = torch.empty(x.shape[0], ql.out_features, dtype=x.dtype, device=x.device)
+    b = None if ql.bias is None else ql.bias.to(x.dtype).contiguous()
+    dt = L.dtype_code(x.dtype)
+    L.check(L.load().ts_qlinear_forward(ctypes.byref(ql._layer), x.data_ptr(), x.shape[0], ql.in_features, dt,
+                                        y.data_ptr(), ql.out_features, dt, L.ptr(b), None, 0, L.stream_ptr()), "fwd")
+    return y
+
+
+@pytest.mark.parametrize("M,dtype,bias", [(17, torch.bfloat16, False), (300, torch.bfloat16, True),
+                                          (520, torch.float16, True)])
+def test_forward_gemm_path(M, dtype, bias):
+    """M > 16 with a workspace: dequantize into it + one library GEMM (bias in
+    the epilogue), against the fused kernel and the float32 reference."""
+    ts = _ts()
+    from tensorshrink_amd import _lib as L
+    ql, W = _layer(768, 1536, 90 + M, NF4)
+    if bias:
+        torch.manual_seed(M)
+        ql.bias = (torch.randn(768) * 0.1).to(dtype).cuda()
+    assert L.load().ts_forward_workspace_bytes(__import__("ctypes").byref(ql._layer), M) >= 768 * 1536 * 2
+    assert L.load().ts_forward_workspace_bytes(__import__("ctypes").byref(ql._layer), 16) == 0
+    x = recipes.activations(M, 1536, seed=M, dtype=dtype).cuda()
+    y = ql(x)
+    y_fused = _forward_no_workspace(ql, x)
+    ref = x.float() @ W.T + (ql.bias.float() if bias else 0)
+    say("gemm path", M, dtype, bias, max_rel_err(y.float(), ref), max_rel_err(y_fused.float(), ref))
+    assert y.dtype == dtype
+    assert max_rel_err(y.float(), ref) <= TOL
+    assert max_rel_err(y_fused.float(), ref) <= TOL
+    assert max_rel_err(y.float(), y_fused.float()) <= TOL
