@@ -25,7 +25,10 @@ Alongside it (extra keys of the same JSON line):
   * "decode_cfg5"  - the same decode step on BASELINE config 5's 70B layer
                      (its 8/4/2-bit mix), 3 rotating copies (1.4 GB);
   * "prefill"      - BASELINE config 4: gate/up/down at M=2048, 8-bit NF8 + DQ
-                     and 6-bit RVQ, 2*M*N*K flops / kernel time vs 2.5 PFLOP/s;
+                     and 6-bit RVQ, 2*M*N*K flops / GPU time vs 2.5 PFLOP/s,
+                     through QuantLinear (dequantize into a workspace +
+                     hipBLASLt GEMM) and, as "fused_kernel", through the
+                     fused MFMA kernel (the same call without a workspace);
   * "quantize"     - BASELINE config 5's GPU GOAP quantize (28672x8192) through
                      the public API, wall time, with the oracle CPU codec timed
                      on a slice;
@@ -257,6 +260,17 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
 
 
+def _forward_fused(q, x):
+    """ts_qlinear_forward without a workspace: the fused MFMA prefill kernel."""
+    import ctypes
+    from tensorshrink_amd import _lib as L
+    y = torch.empty(x.shape[0], q.out_features, dtype=x.dtype, device=x.device)
+    dt = L.dtype_code(x.dtype)
+    L.check(L.load().ts_qlinear_forward(ctypes.byref(q._layer), x.data_ptr(), x.shape[0], q.in_features, dt,
+                                        y.data_ptr(), q.out_features, dt, None, None, 0, L.stream_ptr()), "fused")
+    return y
+
+
 def bench_prefill(args):
     import recipes
     import tensorshrink_amd as ts
@@ -270,28 +284,34 @@ def bench_prefill(args):
             lins.append((name, ts.QuantLinear(ts.quantize_tensor(w, **opts))))
             del w
         xs = {4096: recipes.activations(M, 4096).cuda(), 14336: recipes.activations(M, 14336).cuda()}
-        for _, q in lins:
-            q(xs[q.in_features])
-        torch.cuda.synchronize()
-        times = {name: [] for name, _ in lins}
-        evs = []
-        for s in range(args.prefill_steps):
-            for name, q in lins:
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                q(xs[q.in_features])
-                e1.record()
-                evs.append((name, e0, e1))
-        torch.cuda.synchronize()
-        for name, e0, e1 in evs[len(lins):]:  # the first round absorbs the empty-queue start
-            times[name].append(e0.elapsed_time(e1))
         flops = {name: 2.0 * M * q.out_features * q.in_features for name, q in lins}
-        tot_f = sum(flops[n] * len(times[n]) for n in times)
-        tot_ms = sum(sum(times[n]) for n in times)
-        tflops = tot_f / (tot_ms * 1e-3) / 1e12
-        res[f"{bits}bit"] = {
-            "tflops": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-            "per_linear_us": {n: round(sum(t) / len(t) * 1e3, 1) for n, t in times.items()}}
+
+        def timed(fwd):
+            for _, q in lins:
+                fwd(q, xs[q.in_features])
+            torch.cuda.synchronize()
+            times = {name: [] for name, _ in lins}
+            evs = []
+            for s in range(args.prefill_steps):
+                for name, q in lins:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    fwd(q, xs[q.in_features])
+                    e1.record()
+                    evs.append((name, e0, e1))
+            torch.cuda.synchronize()
+            for name, e0, e1 in evs[len(lins):]:  # the first round absorbs the empty-queue start
+                times[name].append(e0.elapsed_time(e1))
+            tot_f = sum(flops[n] * len(times[n]) for n in times)
+            tot_ms = sum(sum(times[n]) for n in times)
+            tflops = tot_f / (tot_ms * 1e-3) / 1e12
+            return {"tflops": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                    "per_linear_us": {n: round(sum(t) / len(t) * 1e3, 1) for n, t in times.items()}}
+
+        r = timed(lambda q, x: q(x))
+        r["path"] = "QuantLinear: dequantize into a workspace + hipBLASLt GEMM"
+        r["fused_kernel"] = timed(_forward_fused)
+        res[f"{bits}bit"] = r
         del lins, xs
         torch.cuda.empty_cache()
     return res
