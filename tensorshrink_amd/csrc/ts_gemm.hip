@@ -22,12 +22,15 @@ int dequantize(const ts_qlayer* L, int mode, const int32_t* oidx, const uint16_t
 namespace {
 
 constexpr size_t GEMM_LT_WS = 32u << 20;  // hipBLASLt workspace reserved after W
+constexpr int GEMM_CANDIDATES = 8;         // heuristic candidates timed per shape
 
 struct Plan {
   hipblasLtMatmulDesc_t desc = nullptr;
   hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
-  hipblasLtMatmulAlgo_t algo{};
-  size_t ws = 0;
+  hipblasLtMatmulHeuristicResult_t cand[GEMM_CANDIDATES];
+  int n_cand = 0;
+  int best = 0;
+  bool tuned = false;
   bool ok = false;
 };
 
@@ -65,16 +68,15 @@ Plan make_plan(hipblasLtHandle_t h, int64_t M, int64_t N, int64_t K, int64_t ldx
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
   const uint64_t wsmax = GEMM_LT_WS;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax, sizeof(wsmax));
-  hipblasLtMatmulHeuristicResult_t res[1];
   int n = 0;
-  const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, 1, res, &n);
+  const hipblasStatus_t st =
+      hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, GEMM_CANDIDATES, p.cand, &n);
   hipblasLtMatmulPreferenceDestroy(pref);
-  if (st != HIPBLAS_STATUS_SUCCESS || n < 1 || res[0].state != HIPBLAS_STATUS_SUCCESS ||
-      res[0].workspaceSize > GEMM_LT_WS)
-    return p;
-  p.algo = res[0].algo;
-  p.ws = res[0].workspaceSize;
-  p.ok = true;
+  if (st != HIPBLAS_STATUS_SUCCESS) return p;
+  for (int i = 0; i < n; ++i)  // keep the usable candidates, in heuristic order
+    if (p.cand[i].state == HIPBLAS_STATUS_SUCCESS && p.cand[i].workspaceSize <= GEMM_LT_WS)
+      p.cand[p.n_cand++] = p.cand[i];
+  p.ok = p.n_cand > 0;
   return p;
 }
 
@@ -116,9 +118,37 @@ int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, 
     hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp, sizeof(bp));
   }
   const float alpha = 1.f, beta = 0.f;
-  if (hipblasLtMatmul(hit->second, p.desc, &alpha, W, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.algo, lt_ws, p.ws, st) !=
-      HIPBLAS_STATUS_SUCCESS)
-    return TS_HIP_ERROR;
+  auto run = [&](int i) {
+    return hipblasLtMatmul(hit->second, p.desc, &alpha, W, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.cand[i].algo, lt_ws,
+                           p.cand[i].workspaceSize, st) == HIPBLAS_STATUS_SUCCESS;
+  };
+  // The first call of a shape outside graph capture times the candidates
+  // (two runs each, on this call's own operands) and keeps the fastest; this
+  // is the only call that waits for the device. Each candidate writes the
+  // same y, so the last one run leaves the right result.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (!p.tuned && p.n_cand > 1 && hipStreamIsCapturing(st, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+      float best_ms = 1e30f;
+      for (int i = 0; i < p.n_cand; ++i) {
+        if (!run(i)) continue;  // warm
+        hipEventRecord(e0, st);
+        const bool ok = run(i) && run(i);
+        hipEventRecord(e1, st);
+        float ms = 0.f;
+        if (ok && hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess &&
+            ms < best_ms) {
+          best_ms = ms;
+          p.best = i;
+        }
+      }
+    }
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    p.tuned = true;
+  }
+  if (!run(p.best)) return TS_HIP_ERROR;
   return TS_OK;
 }
 
