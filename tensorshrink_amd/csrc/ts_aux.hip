@@ -74,102 +74,134 @@ __global__ void dequant_base_kernel(const ts_qlayer L, void* out, int64_t ldw, i
   }
 }
 
-// Pass 1, vectorised: one thread per 32 consecutive columns of a row (inside
-// one group: group sizes are multiples of 32), its codes in one 8/16/32-byte
-// load, scale/gmin once, 16-byte stores. Same float32 operations as
-// base_value / stage2_value, in the same order, so the output is
-// bit-identical.
-constexpr int DQV_COLS = 32;
-
-template <int BITS>
-TS_DEV void load_codes32(const uint8_t* p, uint32_t (&c)[32]) {
-  if constexpr (BITS == 8) {
-    const ts_u32x4 a = ts_ld16(p), b = ts_ld16(p + 16);
-    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 32; ++i) c[i] = (w[i >> 2] >> (8 * (i & 3))) & 0xffu;
-  } else if constexpr (BITS == 4) {
-    const ts_u32x4 a = ts_ld16(p);
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int i = 0; i < 32; ++i) c[i] = (w[i >> 3] >> (4 * (i & 7))) & 15u;
+// Pass 1, vectorised: 8-column chunks (inside one group), the codes in one
+// 2/4/8-byte load, scale/gmin once per chunk, one 16-byte store (two for
+// f32). Same float32 operations as base_value / stage2_value, in the same
+// order, so the output is bit-identical.
+// Two floats -> packed (lo, hi) bf16 / f16, round to nearest even, the same
+// bits as ts_f2bf / ts_f2h: bf16 through one v_cvt_pk_bf16_f32, with a NaN
+// replaced by ts_f2bf's canonical 0x7fc0.
+template <int DT>
+TS_DEV uint32_t pack_pair(float a, float b) {
+  if constexpr (DT == TS_BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {a, b};
+    uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    if (__builtin_isnan(a) || __builtin_isnan(b))
+      r = (__builtin_isnan(a) ? 0x7fc0u : (r & 0xffffu)) | ((__builtin_isnan(b) ? 0x7fc0u : (r >> 16)) << 16);
+    return r;
   } else {
-    const ts_u32x2 a = ts_ld8(p);
-    const uint32_t w[2] = {a.x, a.y};
-#pragma unroll
-    for (int i = 0; i < 32; ++i) c[i] = (w[i >> 4] >> (2 * (i & 15))) & 3u;
+    return (uint32_t)ts_f2h(a) | ((uint32_t)ts_f2h(b) << 16);
   }
 }
 
-// BITS: 2, 4, 8, or 6 (4-bit stage 1 + 2-bit stage 2)
+// Index math of the vectorised pass in 32 bits (the host checks the sizes);
+// group sizes are powers of two, the double-quant group size usually.
+struct DqvGeom {
+  uint32_t cpr;       // 8-column chunks per row
+  uint32_t nchunks;   // rows x cpr
+  uint32_t gshift;    // log2(group_size)
+  uint32_t dqshift;   // log2(dq_group_size), or 0xff: divide
+};
+
+// One 8-column chunk (inside one group: group sizes are multiples of 8).
 template <int BITS, int DT>
-__global__ __launch_bounds__(256) void dequant_vec_kernel(const ts_qlayer L, void* out, int64_t ldw, int64_t cpr) {
+TS_DEV void dequant_chunk(const ts_qlayer& L, const float* cbs, bool use_cb, const DqvGeom& g, uint32_t ci, void* out,
+                          int64_t ldw) {
 #pragma clang fp contract(off)
-  __shared__ float cbs[256];
-  const bool use_cb = L.codebook && BITS != 6;
-  if (use_cb) {
-    for (int i = threadIdx.x; i < (1 << (BITS == 6 ? 4 : BITS)); i += blockDim.x) cbs[i] = L.codebook[i];
-  }
-  __syncthreads();
-  const int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (q >= L.rows * cpr) return;
-  const int64_t row = q / cpr;
-  const int64_t col0 = (q - row * cpr) * DQV_COLS;
+  const uint32_t row = ci / g.cpr;
+  const uint32_t col0 = (ci - row * g.cpr) * 8u;
+  const uint32_t flat = row * (uint32_t)L.n_groups + (col0 >> g.gshift);
   float s, gm;
-  scale_gmin_f32(L, row, col0 / L.group_size, s, gm);
-  constexpr int B1 = BITS == 6 ? 4 : BITS;
-  uint32_t c[32];
-  load_codes32<B1>(L.packed + row * L.packed_stride + col0 * B1 / 8, c);
-  float v[32];
+  if (L.dq_scale_codes) {  // scale_gmin_f32
+    const uint32_t sup = g.dqshift != 0xffu ? flat >> g.dqshift : flat / (uint32_t)L.dq_group_size;
+    const uint32_t ms = *reinterpret_cast<const uint32_t*>(L.dq_scale_meta + 2 * sup);
+    const uint32_t mg = *reinterpret_cast<const uint32_t*>(L.dq_gmin_meta + 2 * sup);
+    s = (float)L.dq_scale_codes[flat] * ts_h2f((uint16_t)ms) + ts_h2f((uint16_t)(ms >> 16));
+    gm = (float)L.dq_gmin_codes[flat] * ts_h2f((uint16_t)mg) + ts_h2f((uint16_t)(mg >> 16));
+  } else {
+    s = ts_h2f(L.scale[flat]);
+    gm = ts_h2f(L.gmin[flat]);
+  }
+  const uint8_t* p = L.packed + (int64_t)row * L.packed_stride;
+  uint32_t c[8];
+  if constexpr (BITS == 8) {
+    const ts_u32x2 w = ts_ld8(p + col0);
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
+    for (int i = 0; i < 8; ++i) c[i] = ((i < 4 ? w.x : w.y) >> (8 * (i & 3))) & 0xffu;
+  } else if constexpr (BITS == 2) {
+    const uint32_t w = *reinterpret_cast<const uint16_t*>(p + col0 / 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = (w >> (2 * i)) & 3u;
+  } else {  // 4-bit codes (and the 4-bit stage 1 of 6-bit RVQ)
+    const uint32_t w = ts_ld4(p + col0 / 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = (w >> (4 * i)) & 15u;
+  }
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
     const float cv = use_cb ? cbs[c[i]] : (float)c[i];
     v[i] = cv * s + gm;
   }
   if constexpr (BITS == 6) {
-    uint32_t c2[32];
-    load_codes32<2>(L.stage2_packed + row * L.stage2_stride + col0 / 4, c2);
-    const int64_t flat = row * L.n_groups + col0 / L.group_size;
+    const uint32_t w2 = *reinterpret_cast<const uint16_t*>(L.stage2_packed + (int64_t)row * L.stage2_stride + col0 / 4);
     const float s2 = ts_h2f(L.stage2_scale[flat]), g2 = ts_h2f(L.stage2_gmin[flat]);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) v[i] = v[i] + ((float)c2[i] * s2 + g2);
+    for (int i = 0; i < 8; ++i) v[i] = v[i] + ((float)((w2 >> (2 * i)) & 3u) * s2 + g2);
   }
-  const int64_t off = row * ldw + col0;
-  if (col0 + DQV_COLS <= L.cols) {
+  const int64_t off = (int64_t)row * ldw + col0;
+  if (col0 + 8u <= (uint32_t)L.cols) {
     if constexpr (DT == TS_F32) {
       float* o = reinterpret_cast<float*>(out) + off;
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        *reinterpret_cast<ts_f32x4*>(o + 4 * j) = ts_f32x4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+      *reinterpret_cast<ts_f32x4*>(o) = ts_f32x4{v[0], v[1], v[2], v[3]};
+      *reinterpret_cast<ts_f32x4*>(o + 4) = ts_f32x4{v[4], v[5], v[6], v[7]};
     } else {
-      uint16_t* o = reinterpret_cast<uint16_t*>(out) + off;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t h[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float a = v[8 * j + 2 * i], b = v[8 * j + 2 * i + 1];
-          h[i] = DT == TS_BF16 ? ((uint32_t)ts_f2bf(a) | ((uint32_t)ts_f2bf(b) << 16))
-                               : ((uint32_t)ts_f2h(a) | ((uint32_t)ts_f2h(b) << 16));
-        }
-        *reinterpret_cast<ts_u32x4*>(o + 8 * j) = ts_u32x4{h[0], h[1], h[2], h[3]};
-      }
+      *reinterpret_cast<ts_u32x4*>(reinterpret_cast<uint16_t*>(out) + off) =
+          ts_u32x4{pack_pair<DT>(v[0], v[1]), pack_pair<DT>(v[2], v[3]), pack_pair<DT>(v[4], v[5]),
+                   pack_pair<DT>(v[6], v[7])};
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 32; ++i)
-      if (col0 + i < L.cols) store_out(out, off + i, DT, v[i]);
+    for (int i = 0; i < 8; ++i)
+      if (col0 + i < (uint32_t)L.cols) store_out(out, off + i, DT, v[i]);
+  }
+}
+
+// BITS: 2, 4, 8, or 6 (4-bit stage 1 + 2-bit stage 2). Each wave covers 256
+// consecutive 8-column chunks, lane l taking chunks l, l + 64, l + 128,
+// l + 192: every load and store instruction of a wave then covers one
+// contiguous span (1 KB of bf16 output per store).
+template <int BITS, int DT>
+__global__ __launch_bounds__(256) void dequant_vec_kernel(const ts_qlayer L, void* out, int64_t ldw, DqvGeom g) {
+  __shared__ float cbs[256];
+  const float* cb = L.codebook;
+  const bool use_cb = cb != nullptr && BITS != 6;
+  if (use_cb) {
+    for (int i = threadIdx.x; i < (1 << (BITS == 6 ? 4 : BITS)); i += blockDim.x) cbs[i] = cb[i];
+  }
+  __syncthreads();
+  const uint32_t base = (blockIdx.x * 4u + (threadIdx.x >> 6)) * 256u + (threadIdx.x & 63u);
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t ci = base + 64u * j;
+    if (ci < g.nchunks) dequant_chunk<BITS, DT>(L, cbs, use_cb, g, ci, out, ldw);
   }
 }
 
 template <int BITS>
 void launch_dequant_vec(const ts_qlayer& L, void* out, int64_t ldw, int dt, hipStream_t st) {
-  const int64_t cpr = ts_cdiv(L.cols, DQV_COLS);
-  const dim3 grid((unsigned)ts_cdiv(L.rows * cpr, 256));
-  if (dt == TS_F32) hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F32>), grid, dim3(256), 0, st, L, out, ldw, cpr);
-  else if (dt == TS_BF16)
-    hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_BF16>), grid, dim3(256), 0, st, L, out, ldw, cpr);
-  else hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F16>), grid, dim3(256), 0, st, L, out, ldw, cpr);
+  DqvGeom g;
+  g.cpr = (uint32_t)ts_cdiv(L.cols, 8);
+  g.nchunks = (uint32_t)(L.rows * g.cpr);
+  g.gshift = (uint32_t)__builtin_ctzll((unsigned long long)L.group_size);
+  const int64_t dqgs = L.dq_group_size;
+  g.dqshift = (dqgs > 0 && (dqgs & (dqgs - 1)) == 0) ? (uint32_t)__builtin_ctzll((unsigned long long)dqgs) : 0xffu;
+  const dim3 grid((unsigned)ts_cdiv(g.nchunks, 1024));
+  if (dt == TS_F32) hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F32>), grid, dim3(256), 0, st, L, out, ldw, g);
+  else if (dt == TS_BF16) hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_BF16>), grid, dim3(256), 0, st, L, out, ldw, g);
+  else hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F16>), grid, dim3(256), 0, st, L, out, ldw, g);
 }
 
 // Pass 2, codec view (codec.py:793-796, 823-846): the outlier position takes
@@ -256,12 +288,18 @@ int dequantize(const ts_qlayer* Lp, int mode, const int32_t* oidx, const uint16_
   // 16-byte stores need 16-byte aligned rows; the 8-column chunks need group
   // sizes that are multiples of 8 and code rows whose loads stay aligned
   const int esz = dt == TS_F32 ? 4 : 2;
-  // code loads of 32 columns: 8 (2-bit), 16 (4-bit) or 32 (8-bit) bytes, so
-  // rows and bases 16-byte aligned (8 for the 2-bit stage-2 plane)
+  // code loads of 8 columns: 2 (2-bit), 4 (4-bit) or 8 (8-bit) bytes, so rows
+  // and bases aligned to 8 (2 for the 2-bit stage-2 plane); 32-bit index
+  // math; power-of-two group size; (scale, min) meta pairs read as one
+  // 4-byte word
   const bool vec = (ldw * esz) % 16 == 0 && (reinterpret_cast<uintptr_t>(w_out) & 15) == 0 &&
-                   L.group_size % DQV_COLS == 0 && (L.packed_stride % 16) == 0 &&
-                   (reinterpret_cast<uintptr_t>(L.packed) & 15) == 0 &&
-                   (L.bits != 6 || ((L.stage2_stride % 8) == 0 && (reinterpret_cast<uintptr_t>(L.stage2_packed) & 7) == 0));
+                   L.rows * L.n_groups < ((int64_t)1 << 31) && L.rows * ts_cdiv(L.cols, 8) < ((int64_t)1 << 31) &&
+                   (L.group_size & (L.group_size - 1)) == 0 &&
+                   (!L.dq_scale_codes || ((reinterpret_cast<uintptr_t>(L.dq_scale_meta) & 3) == 0 &&
+                                          (reinterpret_cast<uintptr_t>(L.dq_gmin_meta) & 3) == 0)) &&
+                   L.group_size % 8 == 0 && (L.packed_stride % 8) == 0 &&
+                   (reinterpret_cast<uintptr_t>(L.packed) & 7) == 0 &&
+                   (L.bits != 6 || ((L.stage2_stride % 2) == 0 && (reinterpret_cast<uintptr_t>(L.stage2_packed) & 1) == 0));
   if (vec) {
     if (L.bits == 2) launch_dequant_vec<2>(L, w_out, ldw, dt, st);
     else if (L.bits == 4) launch_dequant_vec<4>(L, w_out, ldw, dt, st);
