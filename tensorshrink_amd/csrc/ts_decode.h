@@ -55,6 +55,7 @@ struct DecodeArgs {
   const uint8_t* dqgc;
   const uint16_t* dqgm;
   uint32_t dq_gs;
+  uint32_t dqm_bytes;        // bytes of dqsm / dqgm (4 per super-group)
   const uint8_t* s2packed;
   int64_t s2stride;
   const uint16_t* s2scale;
@@ -247,7 +248,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
 #define TS_PS(f) ts_pin_scalar(a.f)
   TS_PG(packed); TS_PG(scale); TS_PG(gmin); TS_PG(dqsc); TS_PG(dqsm); TS_PG(dqgc); TS_PG(dqgm); TS_PG(x); TS_PG(y);
   TS_PG(slots); TS_PG(cbsrc); TS_PG(bias_src);
-  TS_PS(pstride); TS_PS(dq_gs); TS_PS(ldx); TS_PS(ldy); TS_PS(N); TS_PS(cols); TS_PS(K); TS_PS(n_groups);
+  TS_PS(pstride); TS_PS(dq_gs); TS_PS(dqm_bytes); TS_PS(ldx); TS_PS(ldy); TS_PS(N); TS_PS(cols); TS_PS(K); TS_PS(n_groups);
   TS_PS(n_tiles); TS_PS(M); TS_PS(cb_mode); TS_PS(cap); TS_PS(bias_mul); TS_PS(y_dtype);
   if constexpr (RVQ) { TS_PG(s2packed); TS_PS(s2stride); TS_PG(s2scale); TS_PG(s2gmin); }
 #undef TS_PG
@@ -367,10 +368,17 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       const uint32_t sup0 = f0 / a.dq_gs;
       const uint32_t sup1 = (f0 + (uint32_t)(any ? nlive - 1 : 0)) / a.dq_gs;
       B.split = (int)min((uint32_t)U, (sup0 + 1) * a.dq_gs - f0);
-      B.smA = *reinterpret_cast<const uint32_t*>(a.dqsm + 2 * sup0);
-      B.smB = *reinterpret_cast<const uint32_t*>(a.dqsm + 2 * sup1);
-      B.gmA = *reinterpret_cast<const uint32_t*>(a.dqgm + 2 * sup0);
-      B.gmB = *reinterpret_cast<const uint32_t*>(a.dqgm + 2 * sup1);
+      // super-groups sup0 and sup0 + 1 in one 8-byte buffer load per array
+      // (raw: nothing here consumes it). sup1 is sup0 or sup0 + 1, and when
+      // it is sup0 every live group is below split, so B is never read (past
+      // the last super-group the buffer load returns zeros).
+      (void)sup1;
+      const ts_u32x2 sm = ts_bld8(ts_rsrc(a.dqsm, a.dqm_bytes), 4u * sup0);
+      const ts_u32x2 gv = ts_bld8(ts_rsrc(a.dqgm, a.dqm_bytes), 4u * sup0);
+      B.smA = sm.x;
+      B.smB = sm.y;
+      B.gmA = gv.x;
+      B.gmB = gv.y;
     } else {
       if constexpr (AL) {
         const Bytes<2 * U> vs = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.scale + rowg + gb0));

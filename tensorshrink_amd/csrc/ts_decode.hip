@@ -18,6 +18,7 @@ static int fill_args(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t l
   a.dqgc = L->dq_gmin_codes;
   a.dqgm = L->dq_gmin_meta;
   a.dq_gs = (uint32_t)(L->dq_group_size > 0 ? L->dq_group_size : 1);
+  a.dqm_bytes = L->dq_scale_codes ? (uint32_t)(ts_cdiv(L->rows * L->n_groups, (int64_t)a.dq_gs) * 4) : 0u;
   a.s2packed = L->stage2_packed;
   a.s2stride = L->stage2_stride;
   a.s2scale = L->stage2_scale;
