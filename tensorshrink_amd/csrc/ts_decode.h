@@ -226,6 +226,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   constexpr int GB = Geo::GB, LB = Geo::LB, GB2 = Geo::GB2, LB2 = Geo::LB2;
   static_assert(U >= 1 && U <= Geo::UMAX && (U & (U - 1)) == 0, "groups per batch");
   constexpr int NMF = (BITS == 8 && CB8) ? GS / 16 : GS / 32;  // MFMAs per group
+  constexpr bool TQ = LB == 4 && !RVQ && U % 4 == 0;            // quarter-transposed code loads
   constexpr int CPM = (BITS == 8 && CB8) ? 4 : 8;              // codes per lane per MFMA
   constexpr bool USE_T4 = (BITS == 4);
   constexpr bool USE_T2 = (BITS == 2) || RVQ;
@@ -295,7 +296,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // Raw loads only: nothing here consumes loaded data, so issuing a batch
   // never waits on memory.
   struct Batch {
-    Bytes<LB> w[U];
+    Bytes<LB> w[TQ ? 1 : U];
+    ts_u32x4 wq[TQ ? U / 4 : 1];    // TQ: whole groups, one per lane quarter
     Bytes<(LB2 > 0 ? LB2 : 1)> w2[U];
     uint32_t sc[NSC], gc[NSC];      // DQ codes (bytes), or f16 scale / gmin bits
     uint32_t smA, smB, gmA, gmB;    // DQ (meta_scale, meta_min) f16 pairs of the two super-groups
@@ -305,6 +307,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     ts_u32x4 xv;                    // XM_DPP: this lane's x chunk of the batch
   };
 
+  // TQ (4-byte quarter-groups: 2-bit group 64, 4-bit group 32): each lane
+  // loads one whole 16-byte group of its row, the group gb + 4 h + q of its
+  // lane quarter q, and the four quarters of a row swap pieces at compute
+  // time (a 4 x 4 transpose of dwords across the wave's four 16-lane rows,
+  // two v_permlane32_swap + two v_permlane16_swap), which leaves lane q with
+  // quarter q of groups gb + 4 h .. + 3: one 16-byte load instead of four
+  // 4-byte ones.
   auto load_batch = [&](int64_t tile, int b, Batch& B) {
     const int gb = g_lo + b * U;
     const bool any = gb < g_hi;
@@ -334,8 +343,17 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       B.live |= live ? (1u << u) : 0u;
       gg[u] = live ? gb + u : gb0;
     }
+    if constexpr (TQ) {
+      const uint8_t* rowp = a.packed + r * a.pstride;
 #pragma unroll
-    for (int u = 0; u < U; ++u) B.w[u] = load_bytes<LB>(wp + (int64_t)gg[u] * GB);
+      for (int h = 0; h < U / 4; ++h) {
+        const int gq = gb + 4 * h + q;
+        B.wq[h] = ts_ld16(rowp + (int64_t)((any && gq < g_hi) ? gq : gb0) * GB);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) B.w[u] = load_bytes<LB>(wp + (int64_t)gg[u] * GB);
+    }
     const int64_t rowg = r * G;
     if constexpr (RVQ) {
 #pragma unroll
@@ -395,9 +413,26 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   };
 
   auto compute_batch = [&](int b, const Batch& B, ts_f32x4& yacc) {
+    // the batch's code dwords per group (TQ: after the quarter transpose)
+    uint32_t wt[TQ ? U : 1];
+    if constexpr (TQ) {
+#pragma unroll
+      for (int h = 0; h < U / 4; ++h) {
+        uint32_t d0 = B.wq[h].x, d1 = B.wq[h].y, d2 = B.wq[h].z, d3 = B.wq[h].w;
+        auto p02 = __builtin_amdgcn_permlane32_swap(d0, d2, false, false);
+        auto p13 = __builtin_amdgcn_permlane32_swap(d1, d3, false, false);
+        auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+        auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+        wt[4 * h + 0] = p01[0];
+        wt[4 * h + 1] = p01[1];
+        wt[4 * h + 2] = p23[0];
+        wt[4 * h + 3] = p23[1];
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int g = g_lo + b * U + u;
+      const uint32_t* wd = TQ ? &wt[u] : B.w[TQ ? 0 : u].d;
       if (!((B.live >> u) & 1u)) break;  // wave-uniform
       float s_, gm_;
       if constexpr (DQ) {  // modules.py:573-579: code * meta_scale + meta_min in float32
@@ -446,21 +481,21 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
         }
         if constexpr (BITS == 4) {
           const int b0 = 4 * j;
-          bv[j] = ts_u32x4{t4[byte_of(B.w[u].d, b0 + 0) * R + rsl], t4[byte_of(B.w[u].d, b0 + 1) * R + rsl],
-                           t4[byte_of(B.w[u].d, b0 + 2) * R + rsl], t4[byte_of(B.w[u].d, b0 + 3) * R + rsl]};
+          bv[j] = ts_u32x4{t4[byte_of(wd, b0 + 0) * R + rsl], t4[byte_of(wd, b0 + 1) * R + rsl],
+                           t4[byte_of(wd, b0 + 2) * R + rsl], t4[byte_of(wd, b0 + 3) * R + rsl]};
         } else if constexpr (BITS == 2) {
-          const uint2 e0 = t2[byte_of(B.w[u].d, 2 * j + 0) * R + rsl];
-          const uint2 e1 = t2[byte_of(B.w[u].d, 2 * j + 1) * R + rsl];
+          const uint2 e0 = t2[byte_of(wd, 2 * j + 0) * R + rsl];
+          const uint2 e1 = t2[byte_of(wd, 2 * j + 1) * R + rsl];
           bv[j] = ts_u32x4{e0.x, e0.y, e1.x, e1.y};
         } else if constexpr (CB8) {
-          bv[j] = ts_u32x4{t8[byte_of(B.w[u].d, 4 * j + 0) * R + rsl], t8[byte_of(B.w[u].d, 4 * j + 1) * R + rsl],
-                           t8[byte_of(B.w[u].d, 4 * j + 2) * R + rsl], t8[byte_of(B.w[u].d, 4 * j + 3) * R + rsl]};
+          bv[j] = ts_u32x4{t8[byte_of(wd, 4 * j + 0) * R + rsl], t8[byte_of(wd, 4 * j + 1) * R + rsl],
+                           t8[byte_of(wd, 4 * j + 2) * R + rsl], t8[byte_of(wd, 4 * j + 3) * R + rsl]};
         } else {
           uint32_t pr[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const float f0 = (float)byte_of(B.w[u].d, 8 * j + 2 * t);
-            const float f1 = (float)byte_of(B.w[u].d, 8 * j + 2 * t + 1);
+            const float f0 = (float)byte_of(wd, 8 * j + 2 * t);
+            const float f1 = (float)byte_of(wd, 8 * j + 2 * t + 1);
             if constexpr (BF16)
               pr[t] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0),
                                             0x07060302u);
