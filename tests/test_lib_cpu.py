@@ -119,3 +119,24 @@ def test_no_gpu_fails_loudly():
     import tensorshrink_amd as ts
     with pytest.raises(RuntimeError, match="GPU"):
         ts.quantize_tensor(recipes.gaussian_weight(8, 128, 0))
+
+
+def test_forward_workspace_bytes():
+    """Host-only sizing of the large-M forward workspace: 0 at decode sizes,
+    else the dequantized layer (rows x cols x 2) plus the GEMM library's
+    32 MiB; 0 for an invalid layer view. No GPU call."""
+    import ctypes
+    L, lib = _lib()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced by the sizing call
+    q = L.QLayer()
+    q.bits, q.group_size, q.rows, q.cols = 4, 128, 14336, 4096
+    q.padded_cols, q.n_groups = 4096, 32
+    q.packed = q.scale = q.gmin = fake
+    q.packed_stride = 2048
+    for M in (1, 16):
+        assert lib.ts_forward_workspace_bytes(ctypes.byref(q), M) == 0
+    need = lib.ts_forward_workspace_bytes(ctypes.byref(q), 17)
+    assert need == 14336 * 4096 * 2 + (32 << 20)
+    assert lib.ts_forward_workspace_bytes(ctypes.byref(q), 2048) == need
+    q.n_groups = 31  # inconsistent view
+    assert lib.ts_forward_workspace_bytes(ctypes.byref(q), 2048) == 0
