@@ -215,7 +215,7 @@ struct DecGeom {
 // Occupancy: at most 128 VGPRs (4 waves per SIMD, 16 per CU), so 1024 waves
 // of 16-row tiles are resident at once across 256 CUs.
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
-          int NB>
+          int NB, int RT>
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) {
   constexpr int NT = 64 * W;
   constexpr bool LOOP = NB == 0;
@@ -244,7 +244,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
 #pragma unroll
   for (int i = 1; i < DEC_GMAX; ++i) li += (i < g.n && bid >= g.tile_end[i - 1]) ? 1 : 0;
   DecodeArgs a = g.a[li];
-  const int64_t tile = bid - (li > 0 ? g.tile_end[li > 0 ? li - 1 : 0] : 0);
+  // RT row tiles per workgroup (tile_end counts workgroups): tiles
+  // RT * (its index in the layer) + 0 .. RT - 1, computed together
+  const int64_t tile = RT * (bid - (li > 0 ? g.tile_end[li > 0 ? li - 1 : 0] : 0));
 #define TS_PG(f) ts_pin_global(a.f)
 #define TS_PS(f) ts_pin_scalar(a.f)
   TS_PG(packed); TS_PG(scale); TS_PG(gmin); TS_PG(dqsc); TS_PG(dqsm); TS_PG(dqgc); TS_PG(dqgm); TS_PG(x); TS_PG(y);
@@ -270,10 +272,10 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   if constexpr (USE_T4) { t4 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
   if constexpr (USE_T2) { t2 = reinterpret_cast<uint2*>(sp); sp += 256 * R * 8; }
   if constexpr (USE_T8) { t8 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
-  float* red = reinterpret_cast<float*>(sp);       // [W][64][4]
-  sp += W * 64 * 4 * 4;
-  float* ys = reinterpret_cast<float*>(sp);        // [16][17]
-  sp += 16 * 17 * 4;
+  float* red = reinterpret_cast<float*>(sp);       // [RT][W][64][4]
+  sp += RT * W * 64 * 4 * 4;
+  float* ys = reinterpret_cast<float*>(sp);        // [RT][16][17]
+  sp += RT * 16 * 17 * 4;
   float* cbs = reinterpret_cast<float*>(sp);       // [256] staged codebook
   sp += 256 * 4;
   uint16_t* xs = reinterpret_cast<uint16_t*>(sp);  // [M][K] staged activations (XLDS)
@@ -412,6 +414,21 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
   };
 
+  // float32 (scale, gmin) of group u of a batch
+  auto group_affine = [&](const Batch& B, int u, float& s_, float& gm_) {
+    if constexpr (DQ) {  // modules.py:573-579: code * meta_scale + meta_min in float32
+      const float cs = (float)(AL ? byte_of(B.sc, u) : B.sc[u]);
+      const float cg = (float)(AL ? byte_of(B.gc, u) : B.gc[u]);
+      const uint32_t ms = u < B.split ? B.smA : B.smB;
+      const uint32_t mg = u < B.split ? B.gmA : B.gmB;
+      s_ = __fadd_rn(__fmul_rn(cs, ts_h2f(ms & 0xffffu)), ts_h2f(ms >> 16));
+      gm_ = __fadd_rn(__fmul_rn(cg, ts_h2f(mg & 0xffffu)), ts_h2f(mg >> 16));
+    } else {
+      s_ = ts_h2f((uint16_t)(AL ? half_of(B.sc, u) : B.sc[u]));
+      gm_ = ts_h2f((uint16_t)(AL ? half_of(B.gc, u) : B.gc[u]));
+    }
+  };
+
   auto compute_batch = [&](int b, const Batch& B, ts_f32x4& yacc) {
     // the batch's code dwords per group (TQ: after the quarter transpose)
     uint32_t wt[TQ ? U : 1];
@@ -435,17 +452,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       const uint32_t* wd = TQ ? &wt[u] : B.w[TQ ? 0 : u].d;
       if (!((B.live >> u) & 1u)) break;  // wave-uniform
       float s_, gm_;
-      if constexpr (DQ) {  // modules.py:573-579: code * meta_scale + meta_min in float32
-        const float cs = (float)(AL ? byte_of(B.sc, u) : B.sc[u]);
-        const float cg = (float)(AL ? byte_of(B.gc, u) : B.gc[u]);
-        const uint32_t ms = u < B.split ? B.smA : B.smB;
-        const uint32_t mg = u < B.split ? B.gmA : B.gmB;
-        s_ = __fadd_rn(__fmul_rn(cs, ts_h2f(ms & 0xffffu)), ts_h2f(ms >> 16));
-        gm_ = __fadd_rn(__fmul_rn(cg, ts_h2f(mg & 0xffffu)), ts_h2f(mg >> 16));
-      } else {
-        s_ = ts_h2f((uint16_t)(AL ? half_of(B.sc, u) : B.sc[u]));
-        gm_ = ts_h2f((uint16_t)(AL ? half_of(B.gc, u) : B.gc[u]));
-      }
+      group_affine(B, u, s_, gm_);
       // Phase 1: every LDS read of the group (x operands and code-table
       // entries) is issued before the first MFMA, so the reads overlap
       // instead of each MFMA waiting out one LDS round trip.
@@ -535,6 +542,52 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
           v = __builtin_fmaf(g2_, ax[i], v);
         }
         yacc[i] = v;
+      }
+    }
+  };
+
+  // RT = 2 (4-bit codes, x read from global memory): the same groups of two
+  // row tiles; each x fragment is loaded once for both tiles' MFMAs and the
+  // x.1 sums are shared, which halves x's bytes per weight byte (at M > 8 x
+  // is 4x the weights per MFMA).
+  auto compute_batch2 = [&](int b, const Batch& B0, const Batch& B1, ts_f32x4& y0, ts_f32x4& y1) {
+    if constexpr (RT == 2 && BITS == 4 && !RVQ && XM == XM_GLOBAL && !TQ) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int g = g_lo + b * U + u;
+        if (!((B0.live >> u) & 1u)) break;  // wave-uniform; both tiles share the groups
+        float s0, gm0, s1, gm1;
+        group_affine(B0, u, s0, gm0);
+        group_affine(B1, u, s1, gm1);
+        const int c0 = g * GS + q * (GS / 4);
+        ts_u32x4 xa[NMF], bv0[NMF], bv1[NMF];
+#pragma unroll
+        for (int j = 0; j < NMF; ++j) {
+          const int col = c0 + j * CPM;
+          const ts_u32x4 v = ts_ld16(xrow_glb + min(col, (int)a.cols - 8));
+          xa[j] = col < a.cols ? v : ts_u32x4{0u, 0u, 0u, 0u};
+          const int b0 = 4 * j;
+          bv0[j] = ts_u32x4{t4[byte_of(B0.w[u].d, b0 + 0) * R + rsl], t4[byte_of(B0.w[u].d, b0 + 1) * R + rsl],
+                            t4[byte_of(B0.w[u].d, b0 + 2) * R + rsl], t4[byte_of(B0.w[u].d, b0 + 3) * R + rsl]};
+          bv1[j] = ts_u32x4{t4[byte_of(B1.w[u].d, b0 + 0) * R + rsl], t4[byte_of(B1.w[u].d, b0 + 1) * R + rsl],
+                            t4[byte_of(B1.w[u].d, b0 + 2) * R + rsl], t4[byte_of(B1.w[u].d, b0 + 3) * R + rsl]};
+        }
+        ts_f32x4 aw0 = {0.f, 0.f, 0.f, 0.f}, aw1 = {0.f, 0.f, 0.f, 0.f}, ax = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NMF; ++j) {
+          aw0 = ts_mfma16x16x32<BF16>(xa[j], bv0[j], aw0);
+          aw1 = ts_mfma16x16x32<BF16>(xa[j], bv1[j], aw1);
+          ax = ts_mfma16x16x32<BF16>(xa[j], ones, ax);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = y0[i];
+          v = __builtin_fmaf(s0, aw0[i], v);
+          y0[i] = __builtin_fmaf(gm0, ax[i], v);
+          float w = y1[i];
+          w = __builtin_fmaf(s1, aw1[i], w);
+          y1[i] = __builtin_fmaf(gm1, ax[i], w);
+        }
       }
     }
   };
@@ -662,6 +715,69 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   }
   ts_lds_barrier();
 
+  if constexpr (RT == 2) {
+    static_assert(NB == 1 && XM == XM_GLOBAL && BITS == 4 && !RVQ && !TQ, "two row tiles: 4-bit, x from global");
+    const int capm1 = max(a.cap - 1, 0);
+    auto load_slot = [&](int64_t t, int i) { return a.slots[t * a.cap + min(i, capm1)]; };
+    auto load_bias = [&](int64_t t) { return a.bias_src[min(t * 16 + (tid & 15), a.N - 1) * a.bias_mul]; };
+    // reduce the waves' partials of tile t (buffers of parity par), outliers,
+    // bias, store; the same steps as the single-tile epilogue below
+    auto epilogue = [&](int64_t t, const ts_f32x4& yv, uint64_t slot0, uint64_t slot1, uint16_t bias_v, int par) {
+      float* rd = red + par * (W * 64 * 4);
+      float* yo = ys + par * (16 * 17);
+      *reinterpret_cast<ts_f32x4*>(rd + (wave * 64 + lane) * 4) = yv;
+      ts_lds_barrier();
+      if (tid < 256) {
+        const int l = tid >> 2, i = tid & 3;
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) acc += rd[(w * 64 + l) * 4 + i];
+        yo[(4 * (l >> 4) + i) * 17 + (l & 15)] = acc;
+      }
+      if (a.cap > 0) {
+        ts_lds_barrier();
+        auto add_slot = [&](uint64_t v) {
+          const uint32_t dbits = (uint32_t)(v >> 48);
+          if (dbits == 0u) return;
+          const uint32_t col = (uint32_t)v, row = (uint32_t)(v >> 32) & 0xffffu;
+          const float d = ts_h2f((uint16_t)dbits);
+          for (int m = 0; m < a.M; ++m) atomicAdd(&yo[m * 17 + row], XT<BF16>::to_f(a.x[(int64_t)m * a.ldx + col]) * d);
+        };
+        if (tid < a.cap) add_slot(slot0);
+        if (tid + NT < a.cap) add_slot(slot1);
+        for (int i = tid + 2 * NT; i < a.cap; i += NT) add_slot(a.slots[t * a.cap + i]);
+      }
+      ts_lds_barrier();
+      if (tid < 16 * a.M) {
+        const int m = tid >> 4, nn = tid & 15;
+        const int64_t r = t * 16 + nn;
+        if (r < a.N) {
+          float v = yo[m * 17 + nn];
+          if (a.bias_mul) v += XT<BF16>::to_f(bias_v);
+          const int64_t off = (int64_t)m * a.ldy + r;
+          if (a.y_dtype == TS_F32) reinterpret_cast<float*>(a.y)[off] = v;
+          else if (a.y_dtype == TS_BF16) reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2bf(v);
+          else reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2h(v);
+        }
+      }
+    };
+    // a missing second tile re-reads the first and is not stored
+    const bool live1 = tile + 1 < a.n_tiles;
+    const int64_t t1 = live1 ? tile + 1 : tile;
+    Batch bufA, bufB;
+    load_batch(tile, 0, bufA);
+    load_batch(t1, 0, bufB);
+    const uint64_t s00 = load_slot(tile, tid), s01 = load_slot(tile, tid + NT);
+    const uint64_t s10 = load_slot(t1, tid), s11 = load_slot(t1, tid + NT);
+    const uint16_t b0v = load_bias(tile), b1v = load_bias(t1);
+    asm volatile("" ::: "memory");
+    ts_f32x4 y1 = {0.f, 0.f, 0.f, 0.f};
+    compute_batch2(0, bufA, bufB, yacc, y1);
+    epilogue(tile, yacc, s00, s01, b0v, 0);
+    if (live1) epilogue(t1, y1, s10, s11, b1v, 1);
+    return;
+  }
+
   // The weight stream starts only now, after the workgroup's barriers: a
   // barrier behind it would wait until every wave had issued all its loads,
   // which under a full memory pipeline is most of the stream, and no wave
@@ -749,26 +865,35 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   }
 }
 
-template <int BITS, bool CB8, bool RVQ, int REP, int W>
+template <int BITS, bool CB8, bool RVQ, int REP, int W, int RT>
 inline size_t decode_smem(int M, int64_t K, bool xlds) {
   constexpr int R = dec_rep(REP, W);
   size_t s = 0;
   if (BITS == 4) s += 256 * R * 4;
   if (BITS == 2 || RVQ) s += 256 * R * 8;
   if (BITS == 8 && CB8) s += 256 * R * 4;
-  s += (size_t)W * 64 * 16;
-  s += 16 * 17 * 4;
+  s += (size_t)RT * W * 64 * 16;
+  s += (size_t)RT * 16 * 17 * 4;
   s += 256 * 4;
   if (xlds) s += ((size_t)M * K * 2 + 1023) / 1024 * 1024;  // whole 1 KB chunks
   return s;
 }
 
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
-          int NB>
-inline int launch_decode_x(const DecodeGroup& g, hipStream_t st) {
+          int NB, int RT = 1>
+inline int launch_decode_x(const DecodeGroup& g_in, hipStream_t st) {
+  // RT row tiles per workgroup: tile_end becomes the cumulative workgroup count
+  DecodeGroup g = g_in;
+  if constexpr (RT > 1) {
+    int64_t acc = 0;
+    for (int l = 0; l < g.n; ++l) {
+      acc += (g.a[l].n_tiles + RT - 1) / RT;
+      g.tile_end[l] = acc;
+    }
+  }
   const DecodeArgs& a = g.a[0];
-  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, W>(a.M, a.K, XM != XM_GLOBAL);
-  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB>;
+  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, W, RT>(a.M, a.K, XM != XM_GLOBAL && XM != XM_DPP);
+  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB, RT>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -840,10 +965,20 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   constexpr bool DPP_OK = UMAX * ((BITS == 8 && CB8) ? GS / 16 : GS / 32) <= 16;
   const bool dpp = DPP_OK && a.M == 1;
   const bool one = (a.n_groups + UMAX - 1) / UMAX <= sh.W;  // one batch per wave
+  // x from global memory at M > 1 with a launch of more than one resident
+  // round: two row tiles per workgroup share each x fragment (4-bit codes),
+  // W the smallest of {4, 8, 16} that gives one batch per wave
+  constexpr bool RT2_OK = BITS == 4 && !RVQ && !CB8 && DecGeom<BITS, GS, RVQ>::LB != 4;
+  const int64_t T1 = (a.n_groups + UMAX - 1) / UMAX;
+  const int w_rt = T1 <= 4 ? 4 : (T1 <= 8 ? 8 : (T1 <= 16 ? 16 : 0));
+  const bool rt2 = RT2_OK && !xlds && a.M > 1 && w_rt > 0 && aligned(UMAX) &&
+                   ((g.tile_end[g.n - 1] + 1) / 2) * w_rt > 4096;
 #define TS_DEC(XMV, DQV, ALV, WV, UV, LP) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, (LP) ? 0 : 2>(g, st)
 #define TS_DEC1(XMV, DQV, ALV, WV, UV) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, 1>(g, st)
+#define TS_DECRT(DQV, WV) \
+  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XM_GLOBAL, DQV, true, WV, UMAX, 1, 2>(g, st)
 #define TS_DEC_ALL(DQV)                                                          \
   do {                                                                           \
     const bool alm = aligned(UMAX);                                              \
@@ -861,6 +996,13 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
         TS_DEC(XM_DPP, DQV, true, 16, UMAX, false);                              \
       }                                                                          \
       if (dpp && alm) TS_DEC(XM_DPP, DQV, true, 16, UMAX, true);                 \
+    }                                                                            \
+    if constexpr (RT2_OK) {                                                      \
+      if (rt2) {                                                                 \
+        if (w_rt == 4) TS_DECRT(DQV, 4);                                         \
+        if (w_rt == 8) TS_DECRT(DQV, 8);                                         \
+        TS_DECRT(DQV, 16);                                                       \
+      }                                                                          \
     }                                                                            \
     if (xlds && sh.ok && alm) {                                                  \
       if (sh.W == 4) {                                                           \
@@ -882,6 +1024,7 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   if (dq) TS_DEC_ALL(true);
   TS_DEC_ALL(false);
 #undef TS_DEC_ALL
+#undef TS_DECRT
 #undef TS_DEC1
 #undef TS_DEC
 }

@@ -269,3 +269,23 @@ def test_forward_gemm_path(M, dtype, bias):
     assert max_rel_err(y.float(), ref) <= TOL
     assert max_rel_err(y_fused.float(), ref) <= TOL
     assert max_rel_err(y.float(), y_fused.float()) <= TOL
+
+
+@pytest.mark.parametrize("M", [9, 16])
+def test_forward_group_two_row_tiles(M):
+    """M > 8 at K = 4096 (x read from global memory) with more tiles than one
+    resident round: two 16-row tiles per workgroup share each x fragment.
+    8200-row layers: an odd tile count (a workgroup with one live tile) and a
+    partial last tile."""
+    ts = _ts()
+    made = [_layer(8200, 4096, 300 + i, NF4) for i in range(2)]
+    qls = [m[0] for m in made]
+    torch.manual_seed(M)
+    qls[1].bias = (torch.randn(8200) * 0.1).to(torch.bfloat16).cuda()
+    x = recipes.activations(M, 4096, seed=M).cuda()
+    ys = ts.QuantLinear.forward_group(qls, x)
+    for ql, (_, W), y in zip(qls, made, ys):
+        ref = x.float() @ W.T + (ql.bias.float() if ql.bias is not None else 0)
+        err = max_rel_err(y.float(), ref)
+        say("two row tiles", M, err)
+        assert err <= TOL, err
