@@ -965,14 +965,14 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   constexpr bool DPP_OK = UMAX * ((BITS == 8 && CB8) ? GS / 16 : GS / 32) <= 16;
   const bool dpp = DPP_OK && a.M == 1;
   const bool one = (a.n_groups + UMAX - 1) / UMAX <= sh.W;  // one batch per wave
-  // x from global memory at M > 1 with a launch of more than one resident
-  // round: two row tiles per workgroup share each x fragment (4-bit codes),
+  // x from global memory at M > 1 with at least half a resident round of
+  // waves: two row tiles per workgroup share each x fragment (4-bit codes),
   // W the smallest of {4, 8, 16} that gives one batch per wave
   constexpr bool RT2_OK = BITS == 4 && !RVQ && !CB8 && DecGeom<BITS, GS, RVQ>::LB != 4;
   const int64_t T1 = (a.n_groups + UMAX - 1) / UMAX;
   const int w_rt = T1 <= 4 ? 4 : (T1 <= 8 ? 8 : (T1 <= 16 ? 16 : 0));
   const bool rt2 = RT2_OK && !xlds && a.M > 1 && w_rt > 0 && aligned(UMAX) &&
-                   ((g.tile_end[g.n - 1] + 1) / 2) * w_rt > 4096;
+                   ((g.tile_end[g.n - 1] + 1) / 2) * w_rt >= 2048;
 #define TS_DEC(XMV, DQV, ALV, WV, UV, LP) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, (LP) ? 0 : 2>(g, st)
 #define TS_DEC1(XMV, DQV, ALV, WV, UV) \
