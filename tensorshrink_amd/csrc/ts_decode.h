@@ -22,7 +22,13 @@
 //         y += s[n,g] * (x . cb[c]) + gmin[n,g] * (x . 1)
 //     with both dot products on the matrix core and s/gmin in float32
 //     (rebuilt from double-quant codes in-register, modules.py:573-579).
-//   * x is staged once per workgroup in LDS when M*K fits, else read per group.
+//   * x at M = 1 comes in one 16-byte load per lane and batch and reaches the
+//     MFMA's A operand through DPP row broadcasts (no LDS); at M > 1 it is
+//     staged once per workgroup in LDS when M*K fits, else read per MFMA from
+//     global memory, with two 16-row tiles per workgroup sharing each
+//     fragment when the launch is large.
+//   * 4-byte quarter-group codes (2-bit group 64, 4-bit group 32) come as one
+//     16-byte load per lane and a cross-row dword transpose.
 //   * Per tile: the waves' partials reduced in LDS, the tile's outliers (its
 //     per-tile slots) added with LDS float atomics, then bias and the
 //     compute-dtype store.
