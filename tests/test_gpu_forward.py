@@ -289,3 +289,17 @@ def test_forward_group_two_row_tiles(M):
         err = max_rel_err(y.float(), ref)
         say("two row tiles", M, err)
         assert err <= TOL, err
+
+
+@pytest.mark.parametrize("bits,gs,dq", [(4, 32, True), (4, 32, False), (2, 64, True)])
+def test_forward_quarter_group_codes(bits, gs, dq):
+    """Layers whose lanes hold 4 code bytes per group (4-bit group 32, 2-bit
+    group 64): one 16-byte load per lane and a transpose across the wave's
+    16-lane rows, at every x path (DPP at M = 1, LDS, global)."""
+    opts = dict(bits=bits, group_size=gs, outlier_frac=0.002, double_quant=dq, nf_quant=bits == 4)
+    ql, W = _layer(520, 3072, 40 + bits + gs, opts)
+    for M in (1, 5, 16):
+        x = recipes.activations(M, 3072, seed=M).cuda()
+        err = max_rel_err(ql(x).float(), x.float() @ W.T)
+        say("quarter groups", bits, gs, dq, M, err)
+        assert err <= TOL, (M, err)
