@@ -732,6 +732,20 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       float* rd = red + par * (W * 64 * 4);
       float* yo = ys + par * (16 * 17);
       *reinterpret_cast<ts_f32x4*>(rd + (wave * 64 + lane) * 4) = yv;
+      if (a.cap > 0) {  // into this wave's own partials, as in the single-tile epilogue
+        float* rw = rd + wave * 64 * 4;
+        auto add_slot = [&](uint64_t v) {
+          const uint32_t dbits = (uint32_t)(v >> 48);
+          if (dbits == 0u) return;
+          const uint32_t col = (uint32_t)v, row = (uint32_t)(v >> 32) & 0xffffu;
+          const float d = ts_h2f((uint16_t)dbits);
+          for (int m = 0; m < a.M; ++m)
+            atomicAdd(&rw[(row + 16 * (m >> 2)) * 4 + (m & 3)], XT<BF16>::to_f(a.x[(int64_t)m * a.ldx + col]) * d);
+        };
+        if (tid < a.cap) add_slot(slot0);
+        if (tid + NT < a.cap) add_slot(slot1);
+        for (int i = tid + 2 * NT; i < a.cap; i += NT) add_slot(a.slots[t * a.cap + i]);
+      }
       ts_lds_barrier();
       if (tid < 256) {
         const int l = tid >> 2, i = tid & 3;
@@ -739,19 +753,6 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
 #pragma unroll
         for (int w = 0; w < W; ++w) acc += rd[(w * 64 + l) * 4 + i];
         yo[(4 * (l >> 4) + i) * 17 + (l & 15)] = acc;
-      }
-      if (a.cap > 0) {
-        ts_lds_barrier();
-        auto add_slot = [&](uint64_t v) {
-          const uint32_t dbits = (uint32_t)(v >> 48);
-          if (dbits == 0u) return;
-          const uint32_t col = (uint32_t)v, row = (uint32_t)(v >> 32) & 0xffffu;
-          const float d = ts_h2f((uint16_t)dbits);
-          for (int m = 0; m < a.M; ++m) atomicAdd(&yo[m * 17 + row], XT<BF16>::to_f(a.x[(int64_t)m * a.ldx + col]) * d);
-        };
-        if (tid < a.cap) add_slot(slot0);
-        if (tid + NT < a.cap) add_slot(slot1);
-        for (int i = tid + 2 * NT; i < a.cap; i += NT) add_slot(a.slots[t * a.cap + i]);
       }
       ts_lds_barrier();
       if (tid < 16 * a.M) {
@@ -829,19 +830,15 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   }
 
   // ---- epilogue: reduce the waves' partials, outliers, bias, store ----------
+  // The tile's outliers are added into this wave's own partials, which it has
+  // just written (a wave's LDS operations complete in order), so the single
+  // barrier before the cross-wave sum covers them too. Entry of token m, row
+  // nn: lane nn + 16 (m / 4), element m % 4 (the MFMA's D layout).
   *reinterpret_cast<ts_f32x4*>(red + (wave * 64 + lane) * 4) = yacc;
-  ts_lds_barrier();
-  if (tid < 256) {  // the tile's 16 x 16 (m, row) outputs
-    const int l = tid >> 2, i = tid & 3;
-    float acc = 0.f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) acc += red[(w * 64 + l) * 4 + i];
-    ys[(4 * (l >> 4) + i) * 17 + (l & 15)] = acc;
-  }
   if (a.cap > 0) {
-    ts_lds_barrier();
     // slot = col | (row in tile) << 32 | f16 delta << 48; a zero delta (an
     // unused slot) adds nothing and is skipped
+    float* rw = red + wave * 64 * 4;
     auto add_slot = [&](uint64_t v) {
       const uint32_t dbits = (uint32_t)(v >> 48);
       if (dbits == 0u) return;
@@ -849,12 +846,20 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       const float d = ts_h2f((uint16_t)dbits);
       for (int m = 0; m < a.M; ++m) {
         const float xv = XLDS ? XT<BF16>::to_f(xs[m * a.K + col]) : XT<BF16>::to_f(a.x[(int64_t)m * a.ldx + col]);
-        atomicAdd(&ys[m * 17 + row], xv * d);
+        atomicAdd(&rw[(row + 16 * (m >> 2)) * 4 + (m & 3)], xv * d);
       }
     };
     if (tid < a.cap) add_slot(slot0);
     if (tid + NT < a.cap) add_slot(slot1);
     for (int i = tid + 2 * NT; i < a.cap; i += NT) add_slot(a.slots[sbase + i]);  // rare: > 2 NT in a tile
+  }
+  ts_lds_barrier();
+  if (tid < 256) {  // the tile's 16 x 16 (m, row) outputs
+    const int l = tid >> 2, i = tid & 3;
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) acc += red[(w * 64 + l) * 4 + i];
+    ys[(4 * (l >> 4) + i) * 17 + (l & 15)] = acc;
   }
   ts_lds_barrier();
   if (tid < 16 * a.M) {
