@@ -280,8 +280,6 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   if constexpr (USE_T8) { t8 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
   float* red = reinterpret_cast<float*>(sp);       // [RT][W][64][4]
   sp += RT * W * 64 * 4 * 4;
-  float* ys = reinterpret_cast<float*>(sp);        // [RT][16][17]
-  sp += RT * 16 * 17 * 4;
   float* cbs = reinterpret_cast<float*>(sp);       // [256] staged codebook
   sp += 256 * 4;
   uint16_t* xs = reinterpret_cast<uint16_t*>(sp);  // [M][K] staged activations (XLDS)
@@ -725,12 +723,11 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     static_assert(NB == 1 && XM == XM_GLOBAL && BITS == 4 && !RVQ && !TQ, "two row tiles: 4-bit, x from global");
     const int capm1 = max(a.cap - 1, 0);
     auto load_slot = [&](int64_t t, int i) { return a.slots[t * a.cap + min(i, capm1)]; };
-    auto load_bias = [&](int64_t t) { return a.bias_src[min(t * 16 + (tid & 15), a.N - 1) * a.bias_mul]; };
+    auto load_bias = [&](int64_t t) { return a.bias_src[min(t * 16 + ((tid >> 2) & 15), a.N - 1) * a.bias_mul]; };
     // reduce the waves' partials of tile t (buffers of parity par), outliers,
     // bias, store; the same steps as the single-tile epilogue below
     auto epilogue = [&](int64_t t, const ts_f32x4& yv, uint64_t slot0, uint64_t slot1, uint16_t bias_v, int par) {
       float* rd = red + par * (W * 64 * 4);
-      float* yo = ys + par * (16 * 17);
       *reinterpret_cast<ts_f32x4*>(rd + (wave * 64 + lane) * 4) = yv;
       if (a.cap > 0) {  // into this wave's own partials, as in the single-tile epilogue
         float* rw = rd + wave * 64 * 4;
@@ -752,21 +749,18 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
         float acc = 0.f;
 #pragma unroll
         for (int w = 0; w < W; ++w) acc += rd[(w * 64 + l) * 4 + i];
-        yo[(4 * (l >> 4) + i) * 17 + (l & 15)] = acc;
-      }
-      ts_lds_barrier();
-      if (tid < 16 * a.M) {
-        const int m = tid >> 4, nn = tid & 15;
+        const int m = 4 * (l >> 4) + i, nn = l & 15;
         const int64_t r = t * 16 + nn;
-        if (r < a.N) {
-          float v = yo[m * 17 + nn];
-          if (a.bias_mul) v += XT<BF16>::to_f(bias_v);
+        if (m < a.M && r < a.N) {
+          if (a.bias_mul) acc += XT<BF16>::to_f(bias_v);
           const int64_t off = (int64_t)m * a.ldy + r;
-          if (a.y_dtype == TS_F32) reinterpret_cast<float*>(a.y)[off] = v;
-          else if (a.y_dtype == TS_BF16) reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2bf(v);
-          else reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2h(v);
+          if (a.y_dtype == TS_F32) reinterpret_cast<float*>(a.y)[off] = acc;
+          else if (a.y_dtype == TS_BF16) reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2bf(acc);
+          else reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2h(acc);
         }
       }
+      // (the second tile's epilogue uses the other half of red, so these
+      // reads need no barrier behind them)
     };
     // a missing second tile re-reads the first and is not stored
     const bool live1 = tile + 1 < a.n_tiles;
@@ -802,7 +796,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   const uint64_t slot1 = a.slots[sbase + min(tid + NT, capm1)];
   // bias of the output this thread stores (16 rows x M; entry 0 of a valid
   // array when there is no bias)
-  const uint16_t bias_v = a.bias_src[min(r0 + (tid & 15), a.N - 1) * a.bias_mul];
+  const uint16_t bias_v = a.bias_src[min(r0 + ((tid >> 2) & 15), a.N - 1) * a.bias_mul];
   // every load above stays here (the compiler would otherwise sink batch B's
   // loads into its conditional compute step and drain the counter there)
   asm volatile("" ::: "memory");
@@ -854,24 +848,21 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     for (int i = tid + 2 * NT; i < a.cap; i += NT) add_slot(a.slots[sbase + i]);  // rare: > 2 NT in a tile
   }
   ts_lds_barrier();
-  if (tid < 256) {  // the tile's 16 x 16 (m, row) outputs
+  // the tile's 16 x 16 (token m, row nn) outputs: the thread that sums one
+  // over the waves also adds the bias and stores it
+  if (tid < 256) {
     const int l = tid >> 2, i = tid & 3;
     float acc = 0.f;
 #pragma unroll
     for (int w = 0; w < W; ++w) acc += red[(w * 64 + l) * 4 + i];
-    ys[(4 * (l >> 4) + i) * 17 + (l & 15)] = acc;
-  }
-  ts_lds_barrier();
-  if (tid < 16 * a.M) {
-    const int m = tid >> 4, nn = tid & 15;
+    const int m = 4 * (l >> 4) + i, nn = l & 15;
     const int64_t r = r0 + nn;
-    if (r < a.N) {
-      float v = ys[m * 17 + nn];
-      if (a.bias_mul) v += XT<BF16>::to_f(bias_v);
+    if (m < a.M && r < a.N) {
+      if (a.bias_mul) acc += XT<BF16>::to_f(bias_v);
       const int64_t off = (int64_t)m * a.ldy + r;
-      if (a.y_dtype == TS_F32) reinterpret_cast<float*>(a.y)[off] = v;
-      else if (a.y_dtype == TS_BF16) reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2bf(v);
-      else reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2h(v);
+      if (a.y_dtype == TS_F32) reinterpret_cast<float*>(a.y)[off] = acc;
+      else if (a.y_dtype == TS_BF16) reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2bf(acc);
+      else reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2h(acc);
     }
   }
 }
@@ -884,7 +875,6 @@ inline size_t decode_smem(int M, int64_t K, bool xlds) {
   if (BITS == 2 || RVQ) s += 256 * R * 8;
   if (BITS == 8 && CB8) s += 256 * R * 4;
   s += (size_t)RT * W * 64 * 16;
-  s += (size_t)RT * 16 * 17 * 4;
   s += 256 * 4;
   if (xlds) s += ((size_t)M * K * 2 + 1023) / 1024 * 1024;  // whole 1 KB chunks
   return s;
