@@ -698,6 +698,14 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
   }
   ts_lds_barrier();
+  if constexpr (USE_T4 && !USE_T2 && R % 4 == 0) {
+    // entry b's R copies are contiguous: four per 16-byte store
+    for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
+      const int b = e / R;
+      const uint32_t v = pack2<BF16>(cbs[b & 15], cbs[b >> 4]);
+      *reinterpret_cast<ts_u32x4*>(t4 + e) = ts_u32x4{v, v, v, v};
+    }
+  } else
   for (int e = tid; e < 256 * R; e += NT) {
     const int b = e / R;
     if constexpr (USE_T4) t4[e] = pack2<BF16>(cbs[b & 15], cbs[b >> 4]);
