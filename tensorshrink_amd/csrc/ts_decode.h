@@ -698,12 +698,29 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
   }
   ts_lds_barrier();
+  // entry b's R copies are contiguous: 16-byte stores of four (u32 entries)
+  // or two (u64 entries) copies at a time
   if constexpr (USE_T4 && !USE_T2 && R % 4 == 0) {
-    // entry b's R copies are contiguous: four per 16-byte store
     for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
       const int b = e / R;
       const uint32_t v = pack2<BF16>(cbs[b & 15], cbs[b >> 4]);
       *reinterpret_cast<ts_u32x4*>(t4 + e) = ts_u32x4{v, v, v, v};
+    }
+  } else if constexpr (USE_T8 && R % 4 == 0) {
+    for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
+      const float v = cbs[e / R];
+      const uint16_t hb = XT<BF16>::from_f(v);
+      const uint16_t lb = XT<BF16>::from_f(v - XT<BF16>::to_f(hb));
+      const uint32_t w = (uint32_t)hb | ((uint32_t)lb << 16);
+      *reinterpret_cast<ts_u32x4*>(t8 + e) = ts_u32x4{w, w, w, w};
+    }
+  } else if constexpr (USE_T2 && !USE_T4 && R % 2 == 0) {
+    for (int e = 2 * tid; e < 256 * R; e += 2 * NT) {
+      const int b = e / R;
+      float v[4];
+      for (int j = 0; j < 4; ++j) v[j] = cbs[(b >> (2 * j)) & 3];  // a 2-bit layer's codebook
+      const uint32_t lo = pack2<BF16>(v[0], v[1]), hi = pack2<BF16>(v[2], v[3]);
+      *reinterpret_cast<ts_u32x4*>(t2 + e) = ts_u32x4{lo, hi, lo, hi};
     }
   } else
   for (int e = tid; e < 256 * R; e += NT) {
