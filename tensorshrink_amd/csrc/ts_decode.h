@@ -751,7 +751,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     auto load_bias = [&](int64_t t) { return a.bias_src[min(t * 16 + ((tid >> 2) & 15), a.N - 1) * a.bias_mul]; };
     // reduce the waves' partials of tile t (buffers of parity par), outliers,
     // bias, store; the same steps as the single-tile epilogue below
-    auto epilogue = [&](int64_t t, const ts_f32x4& yv, uint64_t slot0, uint64_t slot1, uint16_t bias_v, int par) {
+    auto epilogue = [&](int64_t t, const ts_f32x4& yv, uint64_t slot0, uint16_t bias_v, int par) {
       float* rd = red + par * (W * 64 * 4);
       *reinterpret_cast<ts_f32x4*>(rd + (wave * 64 + lane) * 4) = yv;
       if (a.cap > 0) {  // into this wave's own partials, as in the single-tile epilogue
@@ -765,8 +765,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
             atomicAdd(&rw[(row + 16 * (m >> 2)) * 4 + (m & 3)], XT<BF16>::to_f(a.x[(int64_t)m * a.ldx + col]) * d);
         };
         if (tid < a.cap) add_slot(slot0);
-        if (tid + NT < a.cap) add_slot(slot1);
-        for (int i = tid + 2 * NT; i < a.cap; i += NT) add_slot(a.slots[t * a.cap + i]);
+        for (int i = tid + NT; i < a.cap; i += NT) add_slot(a.slots[t * a.cap + i]);
       }
       ts_lds_barrier();
       if (tid < 256) {
@@ -793,14 +792,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     Batch bufA, bufB;
     load_batch(tile, 0, bufA);
     load_batch(t1, 0, bufB);
-    const uint64_t s00 = load_slot(tile, tid), s01 = load_slot(tile, tid + NT);
-    const uint64_t s10 = load_slot(t1, tid), s11 = load_slot(t1, tid + NT);
+    const uint64_t s00 = load_slot(tile, tid), s10 = load_slot(t1, tid);
     const uint16_t b0v = load_bias(tile), b1v = load_bias(t1);
     asm volatile("" ::: "memory");
     ts_f32x4 y1 = {0.f, 0.f, 0.f, 0.f};
     compute_batch2(0, bufA, bufB, yacc, y1);
-    epilogue(tile, yacc, s00, s01, b0v, 0);
-    if (live1) epilogue(t1, y1, s10, s11, b1v, 1);
+    epilogue(tile, yacc, s00, b0v, 0);
+    if (live1) epilogue(t1, y1, s10, b1v, 1);
     return;
   }
 
@@ -813,12 +811,11 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   load_batch(tile, 0, bufA);
   if constexpr (NB != 1) load_batch(tile, 1, bufB);  // (a dead batch when nb == 1)
   // This tile's outlier slots sit at a fixed address (no dependent load):
-  // each thread takes slots tid and tid + NT; more (rare) are read in the
-  // epilogue. Indices past cap read a valid slot whose value is dropped.
+  // each thread takes slot tid; more (rare: over NT in a tile) are read in
+  // the epilogue. Indices past cap read a valid slot whose value is dropped.
   const int64_t sbase = tile * a.cap;
   const int capm1 = max(a.cap - 1, 0);
   const uint64_t slot0 = a.slots[sbase + min(tid, capm1)];
-  const uint64_t slot1 = a.slots[sbase + min(tid + NT, capm1)];
   // bias of the output this thread stores (16 rows x M; entry 0 of a valid
   // array when there is no bias)
   const uint16_t bias_v = a.bias_src[min(r0 + ((tid >> 2) & 15), a.N - 1) * a.bias_mul];
@@ -869,8 +866,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       }
     };
     if (tid < a.cap) add_slot(slot0);
-    if (tid + NT < a.cap) add_slot(slot1);
-    for (int i = tid + 2 * NT; i < a.cap; i += NT) add_slot(a.slots[sbase + i]);  // rare: > 2 NT in a tile
+    for (int i = tid + NT; i < a.cap; i += NT) add_slot(a.slots[sbase + i]);  // rare: > NT in a tile
   }
   ts_lds_barrier();
   // the tile's 16 x 16 (token m, row nn) outputs: the thread that sums one
