@@ -184,6 +184,9 @@ TS_DEV uint32_t half_of(const uint32_t* d, int i) { return (d[i >> 1] >> (16 * (
 // workgroup fills a CU (16 waves); with fewer waves per workgroup several
 // workgroups share the CU's LDS and get fewer copies.
 constexpr int dec_rep(int rep, int w) { return rep >= 32 ? (w >= 16 ? 32 : (w >= 8 ? 16 : 4)) : rep; }
+// With x in registers (XM_DPP) the LDS holds only the tables: four 4-wave
+// workgroups per CU fit 16 copies each.
+constexpr int dec_rep_x(int rep, int w, int xm) { return (xm == 3 && rep >= 32 && w == 4) ? 16 : dec_rep(rep, w); }
 
 template <int BITS, int GS, bool RVQ>
 struct DecGeom {
@@ -225,7 +228,7 @@ template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) {
   constexpr int NT = 64 * W;
   constexpr bool LOOP = NB == 0;
-  constexpr int R = dec_rep(REP, W);  // table copies
+  constexpr int R = dec_rep_x(REP, W, XM);  // table copies
   constexpr bool XLDS = XM != XM_GLOBAL && XM != XM_DPP;
   extern __shared__ __align__(16) unsigned char smem[];
   using Geo = DecGeom<BITS, GS, RVQ>;
@@ -888,9 +891,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   }
 }
 
-template <int BITS, bool CB8, bool RVQ, int REP, int W, int RT>
+template <int BITS, bool CB8, bool RVQ, int REP, int XM, int W, int RT>
 inline size_t decode_smem(int M, int64_t K, bool xlds) {
-  constexpr int R = dec_rep(REP, W);
+  constexpr int R = dec_rep_x(REP, W, XM);
   size_t s = 0;
   if (BITS == 4) s += 256 * R * 4;
   if (BITS == 2 || RVQ) s += 256 * R * 8;
@@ -914,7 +917,7 @@ inline int launch_decode_x(const DecodeGroup& g_in, hipStream_t st) {
     }
   }
   const DecodeArgs& a = g.a[0];
-  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, W, RT>(a.M, a.K, XM != XM_GLOBAL && XM != XM_DPP);
+  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, XM, W, RT>(a.M, a.K, XM != XM_GLOBAL && XM != XM_DPP);
   auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB, RT>;
   static bool attr_set = false;
   if (!attr_set) {
