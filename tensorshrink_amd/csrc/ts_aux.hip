@@ -105,54 +105,81 @@ struct DqvGeom {
   uint32_t dqshift;   // log2(dq_group_size), or 0xff: divide
 };
 
-// One 8-column chunk (inside one group: group sizes are multiples of 8).
-template <int BITS, int DT>
-TS_DEV void dequant_chunk(const ts_qlayer& L, const float* cbs, bool use_cb, const DqvGeom& g, uint32_t ci, void* out,
-                          int64_t ldw) {
-#pragma clang fp contract(off)
-  const uint32_t row = ci / g.cpr;
-  const uint32_t col0 = (ci - row * g.cpr) * 8u;
-  const uint32_t flat = row * (uint32_t)L.n_groups + (col0 >> g.gshift);
-  float s, gm;
-  if (L.dq_scale_codes) {  // scale_gmin_f32
-    const uint32_t sup = g.dqshift != 0xffu ? flat >> g.dqshift : flat / (uint32_t)L.dq_group_size;
-    const uint32_t ms = *reinterpret_cast<const uint32_t*>(L.dq_scale_meta + 2 * sup);
-    const uint32_t mg = *reinterpret_cast<const uint32_t*>(L.dq_gmin_meta + 2 * sup);
-    s = (float)L.dq_scale_codes[flat] * ts_h2f((uint16_t)ms) + ts_h2f((uint16_t)(ms >> 16));
-    gm = (float)L.dq_gmin_codes[flat] * ts_h2f((uint16_t)mg) + ts_h2f((uint16_t)(mg >> 16));
+// Raw inputs of one 8-column chunk (inside one group: group sizes are
+// multiples of 8). A lane loads all of its chunks before it stores any: the
+// stores may alias the loads as far as the compiler knows, so loads written
+// after a store stay after it, and a wave would then hold one chunk's loads
+// in flight at a time.
+struct DqChunk {
+  uint32_t row, col0, flat;
+  ts_u32x2 code;   // 8 codes: 8 bytes (8-bit), .x (4-bit), .x low half (2-bit)
+  uint32_t sc, gc;  // DQ: u8 scale/gmin codes; otherwise f16 scale/gmin bits
+  uint32_t ms, mg;  // DQ: (mult, offset) f16 pairs of the super-group
+  uint32_t w2, s2, g2;  // RVQ stage 2: 8 2-bit codes, f16 scale/gmin bits
+};
+
+template <int BITS, bool DQ>
+TS_DEV void dequant_chunk_load(const ts_qlayer& L, const DqvGeom& g, uint32_t ci, DqChunk& c) {
+  c.row = ci / g.cpr;
+  c.col0 = (ci - c.row * g.cpr) * 8u;
+  c.flat = c.row * (uint32_t)L.n_groups + (c.col0 >> g.gshift);
+  if constexpr (DQ) {  // scale_gmin_f32
+    const uint32_t sup = g.dqshift != 0xffu ? c.flat >> g.dqshift : c.flat / (uint32_t)L.dq_group_size;
+    c.ms = *reinterpret_cast<const uint32_t*>(L.dq_scale_meta + 2 * sup);
+    c.mg = *reinterpret_cast<const uint32_t*>(L.dq_gmin_meta + 2 * sup);
+    c.sc = L.dq_scale_codes[c.flat];
+    c.gc = L.dq_gmin_codes[c.flat];
   } else {
-    s = ts_h2f(L.scale[flat]);
-    gm = ts_h2f(L.gmin[flat]);
+    c.sc = L.scale[c.flat];
+    c.gc = L.gmin[c.flat];
   }
-  const uint8_t* p = L.packed + (int64_t)row * L.packed_stride;
-  uint32_t c[8];
+  const uint8_t* p = L.packed + (int64_t)c.row * L.packed_stride;
+  if constexpr (BITS == 8) c.code = ts_ld8(p + c.col0);
+  else if constexpr (BITS == 2) c.code.x = *reinterpret_cast<const uint16_t*>(p + c.col0 / 4);
+  else c.code.x = ts_ld4(p + c.col0 / 2);  // 4-bit codes (and the 4-bit stage 1 of 6-bit RVQ)
+  if constexpr (BITS == 6) {
+    c.w2 = *reinterpret_cast<const uint16_t*>(L.stage2_packed + (int64_t)c.row * L.stage2_stride + c.col0 / 4);
+    c.s2 = L.stage2_scale[c.flat];
+    c.g2 = L.stage2_gmin[c.flat];
+  }
+}
+
+template <int BITS, int DT, bool DQ>
+TS_DEV void dequant_chunk_store(const ts_qlayer& L, const float* cbs, bool use_cb, const DqChunk& c, void* out,
+                                int64_t ldw) {
+#pragma clang fp contract(off)
+  float s, gm;
+  if constexpr (DQ) {
+    s = (float)c.sc * ts_h2f((uint16_t)c.ms) + ts_h2f((uint16_t)(c.ms >> 16));
+    gm = (float)c.gc * ts_h2f((uint16_t)c.mg) + ts_h2f((uint16_t)(c.mg >> 16));
+  } else {
+    s = ts_h2f((uint16_t)c.sc);
+    gm = ts_h2f((uint16_t)c.gc);
+  }
+  uint32_t k[8];
   if constexpr (BITS == 8) {
-    const ts_u32x2 w = ts_ld8(p + col0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) c[i] = ((i < 4 ? w.x : w.y) >> (8 * (i & 3))) & 0xffu;
+    for (int i = 0; i < 8; ++i) k[i] = ((i < 4 ? c.code.x : c.code.y) >> (8 * (i & 3))) & 0xffu;
   } else if constexpr (BITS == 2) {
-    const uint32_t w = *reinterpret_cast<const uint16_t*>(p + col0 / 4);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) c[i] = (w >> (2 * i)) & 3u;
-  } else {  // 4-bit codes (and the 4-bit stage 1 of 6-bit RVQ)
-    const uint32_t w = ts_ld4(p + col0 / 2);
+    for (int i = 0; i < 8; ++i) k[i] = (c.code.x >> (2 * i)) & 3u;
+  } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) c[i] = (w >> (4 * i)) & 15u;
+    for (int i = 0; i < 8; ++i) k[i] = (c.code.x >> (4 * i)) & 15u;
   }
   float v[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float cv = use_cb ? cbs[c[i]] : (float)c[i];
+    const float cv = use_cb ? cbs[k[i]] : (float)k[i];
     v[i] = cv * s + gm;
   }
   if constexpr (BITS == 6) {
-    const uint32_t w2 = *reinterpret_cast<const uint16_t*>(L.stage2_packed + (int64_t)row * L.stage2_stride + col0 / 4);
-    const float s2 = ts_h2f(L.stage2_scale[flat]), g2 = ts_h2f(L.stage2_gmin[flat]);
+    const float s2 = ts_h2f((uint16_t)c.s2), g2 = ts_h2f((uint16_t)c.g2);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = v[i] + ((float)((w2 >> (2 * i)) & 3u) * s2 + g2);
+    for (int i = 0; i < 8; ++i) v[i] = v[i] + ((float)((c.w2 >> (2 * i)) & 3u) * s2 + g2);
   }
-  const int64_t off = (int64_t)row * ldw + col0;
-  if (col0 + 8u <= (uint32_t)L.cols) {
+  const int64_t off = (int64_t)c.row * ldw + c.col0;
+  if (c.col0 + 8u <= (uint32_t)L.cols) {
     if constexpr (DT == TS_F32) {
       float* o = reinterpret_cast<float*>(out) + off;
       *reinterpret_cast<ts_f32x4*>(o) = ts_f32x4{v[0], v[1], v[2], v[3]};
@@ -165,15 +192,16 @@ TS_DEV void dequant_chunk(const ts_qlayer& L, const float* cbs, bool use_cb, con
   } else {
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      if (col0 + i < (uint32_t)L.cols) store_out(out, off + i, DT, v[i]);
+      if (c.col0 + i < (uint32_t)L.cols) store_out(out, off + i, DT, v[i]);
   }
 }
 
 // BITS: 2, 4, 8, or 6 (4-bit stage 1 + 2-bit stage 2). Each wave covers 256
 // consecutive 8-column chunks, lane l taking chunks l, l + 64, l + 128,
 // l + 192: every load and store instruction of a wave then covers one
-// contiguous span (1 KB of bf16 output per store).
-template <int BITS, int DT>
+// contiguous span (1 KB of bf16 output per store). Chunks past the end load
+// the last chunk's inputs (in bounds) and store nothing.
+template <int BITS, int DT, bool DQ>
 __global__ __launch_bounds__(256) void dequant_vec_kernel(const ts_qlayer L, void* out, int64_t ldw, DqvGeom g) {
   __shared__ float cbs[256];
   const float* cb = L.codebook;
@@ -181,13 +209,22 @@ __global__ __launch_bounds__(256) void dequant_vec_kernel(const ts_qlayer L, voi
   if (use_cb) {
     for (int i = threadIdx.x; i < (1 << (BITS == 6 ? 4 : BITS)); i += blockDim.x) cbs[i] = cb[i];
   }
-  __syncthreads();
   const uint32_t base = (blockIdx.x * 4u + (threadIdx.x >> 6)) * 256u + (threadIdx.x & 63u);
+  DqChunk c[4];
 #pragma unroll
-  for (uint32_t j = 0; j < 4; ++j) {
-    const uint32_t ci = base + 64u * j;
-    if (ci < g.nchunks) dequant_chunk<BITS, DT>(L, cbs, use_cb, g, ci, out, ldw);
-  }
+  for (uint32_t j = 0; j < 4; ++j) dequant_chunk_load<BITS, DQ>(L, g, min(base + 64u * j, g.nchunks - 1u), c[j]);
+  __syncthreads();
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j)
+    if (base + 64u * j < g.nchunks) dequant_chunk_store<BITS, DT, DQ>(L, cbs, use_cb, c[j], out, ldw);
+}
+
+template <int BITS, bool DQ>
+void launch_dequant_vec_dt(const ts_qlayer& L, void* out, int64_t ldw, int dt, const DqvGeom& g, dim3 grid,
+                           hipStream_t st) {
+  if (dt == TS_F32) hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F32, DQ>), grid, dim3(256), 0, st, L, out, ldw, g);
+  else if (dt == TS_BF16) hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_BF16, DQ>), grid, dim3(256), 0, st, L, out, ldw, g);
+  else hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F16, DQ>), grid, dim3(256), 0, st, L, out, ldw, g);
 }
 
 template <int BITS>
@@ -199,9 +236,8 @@ void launch_dequant_vec(const ts_qlayer& L, void* out, int64_t ldw, int dt, hipS
   const int64_t dqgs = L.dq_group_size;
   g.dqshift = (dqgs > 0 && (dqgs & (dqgs - 1)) == 0) ? (uint32_t)__builtin_ctzll((unsigned long long)dqgs) : 0xffu;
   const dim3 grid((unsigned)ts_cdiv(g.nchunks, 1024));
-  if (dt == TS_F32) hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F32>), grid, dim3(256), 0, st, L, out, ldw, g);
-  else if (dt == TS_BF16) hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_BF16>), grid, dim3(256), 0, st, L, out, ldw, g);
-  else hipLaunchKernelGGL((dequant_vec_kernel<BITS, TS_F16>), grid, dim3(256), 0, st, L, out, ldw, g);
+  if (L.dq_scale_codes) launch_dequant_vec_dt<BITS, true>(L, out, ldw, dt, g, grid, st);
+  else launch_dequant_vec_dt<BITS, false>(L, out, ldw, dt, g, grid, st);
 }
 
 // Pass 2, codec view (codec.py:793-796, 823-846): the outlier position takes
