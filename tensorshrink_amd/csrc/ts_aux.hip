@@ -204,16 +204,18 @@ TS_DEV void dequant_chunk_store(const ts_qlayer& L, const float* cbs, bool use_c
 template <int BITS, int DT, bool DQ>
 __global__ __launch_bounds__(256) void dequant_vec_kernel(const ts_qlayer L, void* out, int64_t ldw, DqvGeom g) {
   __shared__ float cbs[256];
+  const uint32_t base = (blockIdx.x * 4u + (threadIdx.x >> 6)) * 256u + (threadIdx.x & 63u);
+  DqChunk c[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) dequant_chunk_load<BITS, DQ>(L, g, min(base + 64u * j, g.nchunks - 1u), c[j]);
+  // the codebook after the chunk loads, so that they are in flight while it
+  // arrives; the barrier waits for LDS only, not for the chunk loads
   const float* cb = L.codebook;
   const bool use_cb = cb != nullptr && BITS != 6;
   if (use_cb) {
     for (int i = threadIdx.x; i < (1 << (BITS == 6 ? 4 : BITS)); i += blockDim.x) cbs[i] = cb[i];
   }
-  const uint32_t base = (blockIdx.x * 4u + (threadIdx.x >> 6)) * 256u + (threadIdx.x & 63u);
-  DqChunk c[4];
-#pragma unroll
-  for (uint32_t j = 0; j < 4; ++j) dequant_chunk_load<BITS, DQ>(L, g, min(base + 64u * j, g.nchunks - 1u), c[j]);
-  __syncthreads();
+  ts_lds_barrier();
 #pragma unroll
   for (uint32_t j = 0; j < 4; ++j)
     if (base + 64u * j < g.nchunks) dequant_chunk_store<BITS, DT, DQ>(L, cbs, use_cb, c[j], out, ldw);

@@ -1,6 +1,8 @@
 """QuantLinear forward on the decode (M <= 16) and prefill (M > 16) kernels:
 max |y - y_ref| / max |y_ref| <= 1e-2 against the reference's
 dequantize-then-matmul in float32/float64."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -245,6 +247,32 @@ def _forward_no_workspace(ql, x):
     L.check(L.load().ts_qlinear_forward(ctypes.byref(ql._layer), x.data_ptr(), x.shape[0], ql.in_features, dt,
                                         y.data_ptr(), ql.out_features, dt, L.ptr(b), None, 0, L.stream_ptr()), "fwd")
     return y
+
+
+@pytest.mark.parametrize("opts", [NF4, dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True,
+                                            nf_quant=True),
+                                  dict(bits=6, group_size=64, outlier_frac=0.002, double_quant=False),
+                                  dict(bits=2, group_size=64, outlier_frac=0.05, double_quant=True),
+                                  dict(bits=4, group_size=32, outlier_frac=0.05, double_quant=False)])
+def test_dequantize_weight_vector_pass_matches_scalar(opts):
+    """QuantLinear view (outlier = base + delta (+ stage 2), modules.py:786-802):
+    the vectorised pass (8-column chunks) against the per-element pass (chosen
+    by a row stride that breaks 16-byte alignment), bit for bit in every
+    output dtype, outliers included. 1032 columns: 129 chunks of 8 per row, so
+    waves straddle rows and the last wave is partial; the 5 % cases put
+    several outliers in one 8-column chunk."""
+    ts = _ts()
+    from tensorshrink_amd import _lib as L
+    ql, _ = _layer(200, 1032, 91, opts)
+    assert ql.outlier_row.numel() > 0
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        fused = ql.dequantize_weight(dt)
+        wide = torch.empty(ql.rows, ql.cols + 1, dtype=dt, device="cuda")
+        L.check(L.lib().ts_dequantize(ctypes.byref(ql._layer), L.TS_DEQ_QLINEAR, None, None, 0, wide.data_ptr(),
+                                      ql.cols + 1, L.dtype_code(dt), L.stream_ptr(wide.device)), "dequantize")
+        ref = wide[:, :ql.cols].contiguous()
+        iv = torch.int32 if dt == torch.float32 else torch.int16
+        assert torch.equal(fused.view(iv), ref.view(iv)), dt
 
 
 @pytest.mark.parametrize("M,dtype,bias", [(17, torch.bfloat16, False), (300, torch.bfloat16, True),
