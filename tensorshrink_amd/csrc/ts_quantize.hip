@@ -346,6 +346,116 @@ static void topk_heap_packed(const int64_t* cidx, const float* cval, int64_t nc,
   }
 }
 
+// The same heap steps again, with the keys and the indices in separate arrays:
+// the sift's dependent loads then touch only the keys (for k = 234 881,
+// 470 KB of 16-bit keys instead of 1.9 MB of packed words, so the deep
+// levels stay in the core's L2), and the index moves are plain stores. The
+// keys are order-preserving codes of non-negative values: f16 or bf16 bits
+// when every value is exactly one, else the float bits; non-negative floats
+// and their bit patterns compare alike (no -0.0, no NaN: the caller checks).
+enum KeyKind { KEY_F16, KEY_BF16, KEY_F32 };
+
+template <typename KT>
+struct SplitHeap {
+  KT* key;
+  uint32_t* ix;
+  // __adjust_heap(first, hole, len, x) followed by __push_heap, as PackedHeap
+  inline void adjust(int64_t hole, int64_t len, KT xk, uint32_t xi) {
+    const int64_t top = hole;
+    int64_t child = hole;
+    while (child < (len - 1) / 2) {
+      child = 2 * (child + 1);
+      const KT r = key[child], l = key[child - 1];
+      const bool left = r > l;  // comp(first[child], first[child - 1]), comp = greater
+      child -= left;
+      key[hole] = left ? l : r;
+      ix[hole] = ix[child];
+      hole = child;
+      __builtin_prefetch(key + 4 * hole + 3);  // grandchildren
+      __builtin_prefetch(key + 8 * hole + 7);  // great-grandchildren
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+      child = 2 * (child + 1);
+      key[hole] = key[child - 1];
+      ix[hole] = ix[child - 1];
+      hole = child - 1;
+    }
+    int64_t parent = (hole - 1) / 2;
+    while (hole > top && key[parent] > xk) {  // comp(first[parent], value)
+      key[hole] = key[parent];
+      ix[hole] = ix[parent];
+      hole = parent;
+      parent = (hole - 1) / 2;
+    }
+    key[hole] = xk;
+    ix[hole] = xi;
+  }
+};
+
+template <typename KT, KeyKind KK>
+static void topk_heap_split(const int64_t* cidx, const float* cval, int64_t nc, int64_t k, int64_t* out_idx,
+                            float* out_val) {
+  auto enc = [](float v) -> KT {
+    if constexpr (KK == KEY_F16) return __builtin_bit_cast(uint16_t, (_Float16)v);
+    else if constexpr (KK == KEY_BF16) return (uint16_t)(__builtin_bit_cast(uint32_t, v) >> 16);
+    else return __builtin_bit_cast(uint32_t, v);
+  };
+  auto dec = [](KT x) -> float {
+    if constexpr (KK == KEY_F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)x);
+    else if constexpr (KK == KEY_BF16) return __builtin_bit_cast(float, (uint32_t)x << 16);
+    else return __builtin_bit_cast(float, (uint32_t)x);
+  };
+  std::vector<KT> kb((size_t)k);
+  std::vector<uint32_t> ib((size_t)k);
+  SplitHeap<KT> H{kb.data(), ib.data()};
+  KT* key = H.key;
+  uint32_t* ix = H.ix;
+  for (int64_t j = 0; j < k; ++j) {
+    key[j] = enc(cval[j]);
+    ix[j] = (uint32_t)cidx[j];
+  }
+  if (k >= 2) {  // __make_heap
+    for (int64_t parent = (k - 2) / 2;; --parent) {
+      H.adjust(parent, k, key[parent], ix[parent]);
+      if (parent == 0) break;
+    }
+  }
+  KT top = key[0];  // __heap_select
+  for (int64_t j = k; j < nc; ++j) {
+    const KT e = enc(cval[j]);
+    if (e > top) {
+      H.adjust(0, k, e, (uint32_t)cidx[j]);
+      top = key[0];
+    }
+  }
+  for (int64_t last = k; last > 1; --last) {  // __sort_heap
+    const KT xk = key[last - 1];
+    const uint32_t xi = ix[last - 1];
+    key[last - 1] = key[0];
+    ix[last - 1] = ix[0];
+    H.adjust(0, last - 1, xk, xi);
+  }
+  for (int64_t j = 0; j < k; ++j) {
+    out_idx[j] = (int64_t)ix[j];
+    out_val[j] = dec(key[j]);
+  }
+}
+
+// Which split-heap keys the stream allows; false: some value is negative,
+// -0.0 or NaN (the packed float heap then runs).
+static bool split_key_kind(const float* cval, int64_t nc, KeyKind* kind) {
+  bool f16 = true, bf16 = true;
+  for (int64_t j = 0; j < nc; ++j) {
+    const float v = cval[j];
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if ((u >> 31) || std::isnan(v)) return false;
+    f16 = f16 && (float)(_Float16)v == v;
+    bf16 = bf16 && (u & 0xffffu) == 0;
+  }
+  *kind = f16 ? KEY_F16 : (bf16 ? KEY_BF16 : KEY_F32);
+  return true;
+}
+
 int topk_select(const int64_t* cidx, const float* cval, int64_t nc, int64_t n, int64_t k, int64_t* out_idx,
                 float* out_val) {
   if (k <= 0 || k > n || nc < k) return TS_BAD_ARG;
@@ -355,7 +465,11 @@ int topk_select(const int64_t* cidx, const float* cval, int64_t nc, int64_t n, i
     bool packable = n <= (int64_t)UINT32_MAX + 1;
     for (int64_t j = 0; j < nc && packable; ++j) packable = !std::isnan(cval[j]);
     if (packable) {
-      topk_heap_packed(cidx, cval, nc, k, out_idx, out_val);
+      KeyKind kk;
+      if (!split_key_kind(cval, nc, &kk)) topk_heap_packed(cidx, cval, nc, k, out_idx, out_val);
+      else if (kk == KEY_F16) topk_heap_split<uint16_t, KEY_F16>(cidx, cval, nc, k, out_idx, out_val);
+      else if (kk == KEY_BF16) topk_heap_split<uint16_t, KEY_BF16>(cidx, cval, nc, k, out_idx, out_val);
+      else topk_heap_split<uint32_t, KEY_F32>(cidx, cval, nc, k, out_idx, out_val);
       return TS_OK;
     }
     // __heap_select: make_heap(first k); for later elements beating the top,

@@ -63,20 +63,41 @@ def _prefix_filter(a, k):
     return keep
 
 
+# The replay keys the heap by the values' f16 bits when every value is a
+# non-negative f16 ("gauss", "ties", "f16sub"), by bf16 bits when every value
+# is a bf16 ("bf16"), by float bits for other non-negative streams ("f32",
+# "f32ties"), and runs the packed float heap for signed ones ("signed") and
+# the std:: calls with NaN ("nan").
 @pytest.mark.parametrize("n,k,kind", [(200000, 200, "gauss"), (120000, 1500, "ties"), (65536, 1024, "ties"),
-                                      (5000, 600, "ties"), (5000, 4999, "gauss"), (100000, 300, "nan")])
+                                      (5000, 600, "ties"), (5000, 4999, "gauss"), (100000, 300, "nan"),
+                                      (120000, 1500, "bf16"), (200000, 200, "f32"), (120000, 1500, "f32ties"),
+                                      (120000, 1500, "f16sub"), (120000, 1500, "signed")])
 def test_topk_select_replay(n, k, kind):
     L, lib = _lib()
     g = torch.Generator().manual_seed(n ^ k)
     if kind == "ties":
         a = (torch.randint(-30, 31, (n,), generator=g).float() / 30).to(torch.float16).float().abs().numpy()
+    elif kind == "bf16":  # beyond f16's range
+        a = (torch.randn(n, generator=g) * 1e6).to(torch.bfloat16).float().abs().numpy()
+    elif kind == "f32":
+        a = torch.randn(n, generator=g).abs().numpy()
+    elif kind == "f32ties":
+        a = (torch.randint(-30, 31, (n,), generator=g).float() * 1.1 / 30).abs().numpy()
+        assert (a.view(np.uint32) & 0xFFFF).any()
+    elif kind == "f16sub":  # f16 subnormals, many ties
+        a = (torch.randn(n, generator=g) * 3e-7).to(torch.float16).float().abs().numpy()
+    elif kind == "signed":
+        a = torch.randn(n, generator=g).to(torch.float16).float().numpy()
     else:
         a = torch.randn(n, generator=g).to(torch.float16).float().abs().numpy()
     if kind == "nan":  # NaN ranks above every number (the std:: path)
         a[[7, 5000, 77777]] = np.nan
-    ov_ref, oi_ref = O.topk_abs(a, k)
     tv, ti = torch.topk(torch.from_numpy(a), k)
-    np.testing.assert_array_equal(oi_ref, ti.numpy())
+    if kind == "signed":  # topk of the values themselves: torch.topk is the reference
+        ov_ref, oi_ref = tv.numpy(), ti.numpy()
+    else:
+        ov_ref, oi_ref = O.topk_abs(a, k)
+        np.testing.assert_array_equal(oi_ref, ti.numpy())
     rc, oi, ov = _select(lib, np.arange(n), a, n, k)
     assert rc == 0
     np.testing.assert_array_equal(oi, oi_ref)
