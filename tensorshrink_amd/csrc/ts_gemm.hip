@@ -6,11 +6,15 @@
 // library GEMM runs near the matrix cores' rate, so materialising W costs
 // less than dequantizing every weight tile once per M-tile inside a fused
 // kernel.
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
+#include <set>
 #include <tuple>
+#include <vector>
 
 #include "ts_common.h"
 
@@ -22,13 +26,14 @@ int dequantize(const ts_qlayer* L, int mode, const int32_t* oidx, const uint16_t
 namespace {
 
 constexpr size_t GEMM_LT_WS = 32u << 20;  // hipBLASLt workspace reserved after W
-constexpr int GEMM_CANDIDATES = 8;         // heuristic candidates timed per shape
+constexpr int GEMM_HEURISTIC = 8;          // heuristic candidates, tried first
+constexpr int GEMM_FINALISTS = 4;          // re-timed candidates of the first pass
 
 struct Plan {
   hipblasLtMatmulDesc_t desc = nullptr;
   hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
-  hipblasLtMatmulHeuristicResult_t cand[GEMM_CANDIDATES];
-  int n_cand = 0;
+  std::vector<hipblasLtMatmulAlgo_t> algo;  // heuristic order, then every other supported algorithm
+  std::vector<size_t> ws;                   // workspace bytes of each
   int best = 0;
   bool tuned = false;
   bool ok = false;
@@ -68,15 +73,39 @@ Plan make_plan(hipblasLtHandle_t h, int64_t M, int64_t N, int64_t K, int64_t ldx
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return p;
   const uint64_t wsmax = GEMM_LT_WS;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax, sizeof(wsmax));
+  hipblasLtMatmulHeuristicResult_t heur[GEMM_HEURISTIC];
   int n = 0;
   const hipblasStatus_t st =
-      hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, GEMM_CANDIDATES, p.cand, &n);
+      hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.a, p.b, p.d, p.d, pref, GEMM_HEURISTIC, heur, &n);
   hipblasLtMatmulPreferenceDestroy(pref);
   if (st != HIPBLAS_STATUS_SUCCESS) return p;
-  for (int i = 0; i < n; ++i)  // keep the usable candidates, in heuristic order
-    if (p.cand[i].state == HIPBLAS_STATUS_SUCCESS && p.cand[i].workspaceSize <= GEMM_LT_WS)
-      p.cand[p.n_cand++] = p.cand[i];
-  p.ok = p.n_cand > 0;
+  std::set<int> seen;
+  for (int i = 0; i < n; ++i)  // the usable heuristic candidates, in its order
+    if (heur[i].state == HIPBLAS_STATUS_SUCCESS && heur[i].workspaceSize <= GEMM_LT_WS) {
+      p.algo.push_back(heur[i].algo);
+      p.ws.push_back(heur[i].workspaceSize);
+      seen.insert(hipblaslt_ext::getIndexFromAlgo(heur[i].algo));
+    }
+  // then every other algorithm of the library that supports this problem
+  std::vector<hipblasLtMatmulHeuristicResult_t> all;
+  const hipDataType tx = hip_type(xdt), ty = hip_type(ydt);
+  if (hipblaslt_ext::getAllAlgos(h, hipblaslt_ext::GemmType::HIPBLASLT_GEMM, HIPBLAS_OP_T, HIPBLAS_OP_N, tx, tx, ty,
+                                 ty, HIPBLAS_COMPUTE_32F, all) == HIPBLAS_STATUS_SUCCESS) {
+    const float alpha = 1.f, beta = 0.f;
+    for (auto& r : all) {
+      const int idx = hipblaslt_ext::getIndexFromAlgo(r.algo);
+      if (idx < 0 || seen.count(idx)) continue;
+      size_t wsb = 0;
+      if (hipblaslt_ext::matmulIsAlgoSupported(h, p.desc, &alpha, p.a, p.b, &beta, p.d, p.d, r.algo, wsb) !=
+              HIPBLAS_STATUS_SUCCESS ||
+          wsb > GEMM_LT_WS)
+        continue;
+      seen.insert(idx);
+      p.algo.push_back(r.algo);
+      p.ws.push_back(wsb);
+    }
+  }
+  p.ok = !p.algo.empty();
   return p;
 }
 
@@ -119,28 +148,41 @@ int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, 
   }
   const float alpha = 1.f, beta = 0.f;
   auto run = [&](int i) {
-    return hipblasLtMatmul(hit->second, p.desc, &alpha, W, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.cand[i].algo, lt_ws,
-                           p.cand[i].workspaceSize, st) == HIPBLAS_STATUS_SUCCESS;
+    return hipblasLtMatmul(hit->second, p.desc, &alpha, W, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.algo[i], lt_ws,
+                           p.ws[i], st) == HIPBLAS_STATUS_SUCCESS;
   };
-  // The first call of a shape outside graph capture times the candidates
-  // (two runs each, on this call's own operands) and keeps the fastest; this
-  // is the only call that waits for the device. Each candidate writes the
-  // same y, so the last one run leaves the right result.
+  // The first call of a shape outside graph capture times the candidates on
+  // this call's own operands and keeps the fastest: one warm and one timed
+  // run each, then the best few again over three runs. This is the only call
+  // that waits for the device. Each candidate writes the same y, so the last
+  // one run leaves the right result. Under capture, before tuning, the
+  // heuristic's first choice runs.
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (!p.tuned && p.n_cand > 1 && hipStreamIsCapturing(st, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
+  const int nc = (int)p.algo.size();
+  if (!p.tuned && nc > 1 && hipStreamIsCapturing(st, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
-      float best_ms = 1e30f;
-      for (int i = 0; i < p.n_cand; ++i) {
-        if (!run(i)) continue;  // warm
+      auto time_of = [&](int i, int reps) -> float {
+        if (!run(i)) return 1e30f;  // warm
         hipEventRecord(e0, st);
-        const bool ok = run(i) && run(i);
+        bool ok = true;
+        for (int r = 0; r < reps; ++r) ok = ok && run(i);
         hipEventRecord(e1, st);
         float ms = 0.f;
-        if (ok && hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess &&
-            ms < best_ms) {
+        if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+          return 1e30f;
+        return ms / reps;
+      };
+      std::vector<std::pair<float, int>> t1;
+      for (int i = 0; i < nc; ++i) t1.emplace_back(time_of(i, 1), i);
+      std::sort(t1.begin(), t1.end());
+      float best_ms = 1e30f;
+      for (int f = 0; f < std::min(nc, GEMM_FINALISTS); ++f) {
+        if (t1[f].first >= 1e30f) break;
+        const float ms = time_of(t1[f].second, 3);
+        if (ms < best_ms) {
           best_ms = ms;
-          p.best = i;
+          p.best = t1[f].second;
         }
       }
     }
