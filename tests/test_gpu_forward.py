@@ -275,6 +275,38 @@ def test_dequantize_weight_vector_pass_matches_scalar(opts):
         assert torch.equal(fused.view(iv), ref.view(iv)), dt
 
 
+@pytest.mark.parametrize("M", [1, 5, 300])
+def test_forward_graph_replay(M):
+    """QuantLinear.forward captured in a HIP graph and replayed four times, with
+    eager work and synchronisation between replays: every replay equals the
+    eager call (decode for M <= 16; dequantize into the workspace + hipBLASLt
+    above, the algorithm chosen by the eager call's tuning)."""
+    ts = _ts()
+    ql, W = _layer(1024, 2048, 77, NF4)
+    ql.bias = torch.randn(ql.out_features, dtype=torch.bfloat16).cuda()
+    x = recipes.activations(M, 2048).cuda()
+    y_eager = ql(x)
+    torch.cuda.synchronize()
+    static_x = x.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ql(static_x)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_y = ql(static_x)
+    ref = x.float() @ W.T + ql.bias.float()
+    for i in range(4):
+        other = ql(x[: max(1, M // 2)])  # eager work between replays
+        g.replay()
+        torch.cuda.synchronize()
+        assert max_rel_err(static_y.float(), y_eager.float()) <= 1e-3, i
+        assert max_rel_err(static_y.float(), ref) <= TOL, i
+        del other
+
+
 @pytest.mark.parametrize("M,dtype,bias", [(17, torch.bfloat16, False), (300, torch.bfloat16, True),
                                           (520, torch.float16, True)])
 def test_forward_gemm_path(M, dtype, bias):
