@@ -25,6 +25,7 @@ from __future__ import annotations
 import ctypes
 import dataclasses
 import math
+import threading
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
@@ -186,8 +187,9 @@ def _to_host(t: torch.Tensor) -> np.ndarray:
     return h.numpy()
 
 
-def _topk_outliers(wg: torch.Tensor, k: int) -> Tuple[np.ndarray, np.ndarray]:
-    """(indices, |w| values) of torch.topk(|w|, k) in CPU order (codec.py:533-535)."""
+def _topk_candidates(wg: torch.Tensor, k: int) -> Tuple[np.ndarray, np.ndarray]:
+    """Host (indices, |w|) of the elements the top-k selection can touch, in
+    index order: the GPU candidate filter, or every element when k > n / 64."""
     lib = L.lib()
     n = wg.numel()
     st = L.stream_ptr()
@@ -202,18 +204,49 @@ def _topk_outliers(wg: torch.Tensor, k: int) -> Tuple[np.ndarray, np.ndarray]:
         cval = torch.empty(nc, dtype=torch.float32, device=wg.device)
         L.check(lib.ts_topk_candidates_write(ctypes.byref(qi), k, ws.data_ptr(), cidx.data_ptr(), cval.data_ptr(),
                                              st), "topk candidates")
-        ci = _to_host(cidx)
-        cv = _to_host(cval)
-    else:
-        # nth_element regime (k > n / 64): the selection needs every element.
-        cv = wg.reshape(-1).to(torch.float32).abs().cpu().numpy()
-        ci = np.arange(n, dtype=np.int64)
-        nc = n
+        return _to_host(cidx), _to_host(cval)
+    # nth_element regime (k > n / 64): the selection needs every element.
+    return np.arange(n, dtype=np.int64), wg.reshape(-1).to(torch.float32).abs().cpu().numpy()
+
+
+def _topk_select(ci: np.ndarray, cv: np.ndarray, n: int, k: int) -> Tuple[np.ndarray, np.ndarray]:
+    """(indices, |w| values) of torch.topk(|w|, k) in CPU order (codec.py:533-535)
+    from the candidate stream (host only; ctypes releases the GIL)."""
     out_i = np.empty(k, np.int64)
     out_v = np.empty(k, np.float32)
-    L.check(lib.ts_topk_select(ci.ctypes.data, cv.ctypes.data, nc, n, k, out_i.ctypes.data, out_v.ctypes.data),
-            "topk select")
+    L.check(L.lib().ts_topk_select(ci.ctypes.data, cv.ctypes.data, cv.shape[0], n, k, out_i.ctypes.data,
+                                   out_v.ctypes.data), "topk select")
     return out_i, out_v
+
+
+def _topk_outliers(wg: torch.Tensor, k: int) -> Tuple[np.ndarray, np.ndarray]:
+    """(indices, |w| values) of torch.topk(|w|, k) in CPU order (codec.py:533-535)."""
+    ci, cv = _topk_candidates(wg, k)
+    return _topk_select(ci, cv, wg.numel(), k)
+
+
+class _Replay(threading.Thread):
+    """The top-k heap replay on a host thread, so that the group encode and
+    the result copies (which need only the clamp threshold) run meanwhile."""
+
+    def __init__(self, ci: np.ndarray, cv: np.ndarray, n: int, k: int):
+        super().__init__(name="ts-topk-replay", daemon=True)
+        self.args = (ci, cv, n, k)
+        self.result = None
+        self.error = None
+        self.start()
+
+    def run(self):
+        try:
+            self.result = _topk_select(*self.args)
+        except BaseException as e:  # re-raised by get()
+            self.error = e
+
+    def get(self) -> Tuple[np.ndarray, np.ndarray]:
+        self.join()
+        if self.error is not None:
+            raise self.error
+        return self.result
 
 
 def _linspace(lo: float, hi: float, n: int, device) -> np.ndarray:
@@ -229,19 +262,18 @@ def _quantize_2d(wg: torch.Tensor, rows: int, cols: int, bits: int, group_size: 
     dev = wg.device
     st = L.stream_ptr()
     n = rows * cols
+    replay = None
     if 0 < k < n:
-        oi, ov = _topk_outliers(wg, k)
-        t = float(ov.min())
-        idx_dev = torch.from_numpy(oi).to(dev)
-        oval = torch.empty(k, dtype=torch.float16, device=dev)
-        L.check(lib.ts_gather_f16(wg.data_ptr(), L.dtype_code(wg.dtype), idx_dev.data_ptr(), k, oval.data_ptr(), st),
-                "outlier values")
-        outlier_idx = oi.astype(np.int32)
-        outlier_val = _to_host(oval)
+        ci, cv = _topk_candidates(wg, k)
+        replay = _Replay(ci, cv, n, k)
+        # The clamp threshold min(topk values) is the k-th largest |w|: every
+        # element above it is a candidate, so the candidates' k-th largest is
+        # the same float. With NaN (ranked first, and min() propagates it) it
+        # waits for the replay.
+        nan = bool(np.isnan(cv).any())
+        t = float(replay.get()[1].min()) if nan else float(np.partition(cv, cv.shape[0] - k)[cv.shape[0] - k])
         clamp = 1
     else:
-        outlier_idx = np.zeros(0, np.int32)
-        outlier_val = np.zeros(0, np.float16)
         t, clamp = 0.0, 0
     pad = (-cols) % group_size
     padded_cols = cols + pad
@@ -286,8 +318,7 @@ def _quantize_2d(wg: torch.Tensor, rows: int, cols: int, bits: int, group_size: 
     opts = L.GroupOpts(bits, group_size, t, clamp, L.ptr(cb_dev), 0 if cb_dev is None else cb_dev.numel())
     L.check(lib.ts_quantize_groups(ctypes.byref(qi), ctypes.byref(opts), packed.data_ptr(), pcols, s16.data_ptr(),
                                    g16.data_ptr(), None, None, st), "group encode")
-    res = dict(rows=rows, cols=cols, padded_cols=padded_cols, n_groups=n_groups, outlier_idx=outlier_idx,
-               outlier_val=outlier_val, codebook=codebook_np)
+    res = dict(rows=rows, cols=cols, padded_cols=padded_cols, n_groups=n_groups, codebook=codebook_np)
     if double_quant:
         nsg = rows * n_groups
         n_super = (nsg + dq_group_size - 1) // dq_group_size
@@ -304,6 +335,19 @@ def _quantize_2d(wg: torch.Tensor, rows: int, cols: int, bits: int, group_size: 
         res["scale"] = _to_host(s16)
         res["gmin"] = _to_host(g16)
     res["packed"] = _to_host(packed)
+    if replay is not None:
+        oi, ov = replay.get()
+        if not nan and float(ov.min()) != t:
+            raise RuntimeError("tensorshrink_amd: top-k threshold disagrees with the replay")
+        idx_dev = torch.from_numpy(oi).to(dev)
+        oval = torch.empty(k, dtype=torch.float16, device=dev)
+        L.check(lib.ts_gather_f16(wg.data_ptr(), L.dtype_code(wg.dtype), idx_dev.data_ptr(), k, oval.data_ptr(), st),
+                "outlier values")
+        res["outlier_idx"] = oi.astype(np.int32)
+        res["outlier_val"] = _to_host(oval)
+    else:
+        res["outlier_idx"] = np.zeros(0, np.int32)
+        res["outlier_val"] = np.zeros(0, np.float16)
     return res
 
 
