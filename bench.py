@@ -60,8 +60,9 @@ def log(*a):
 
 
 def layer_bytes(ql, M: int) -> int:
-    """Algorithmic bytes of one decode launch: packed + metadata + outliers +
-    codebook + x + y (+ bias), as in the survey's measurement section."""
+    """Algorithmic bytes of one decode launch: every byte the launch must move
+    once, i.e. packed codes + metadata + outlier tables + codebook + x + y
+    (+ bias)."""
     N, K = ql.out_features, ql.in_features
     b = ql.packed.numel()
     if ql.double_quant:
