@@ -114,6 +114,30 @@ def test_topk_select_replay(n, k, kind):
         assert rc == L.TS_BAD_ARG
 
 
+@pytest.mark.parametrize("kind", ["ties", "gauss", "bf16", "f32"])
+def test_clamp_threshold_from_candidates(kind):
+    """quantize_tensor takes the clamp threshold min(top-k |w|) as the k-th
+    largest candidate (np.partition) while the replay runs: every element above
+    the k-th largest |w| is a candidate, so the two agree on filtered streams."""
+    L, lib = _lib()
+    n, k = 120000, 1500
+    g = torch.Generator().manual_seed(7 + len(kind))
+    if kind == "ties":
+        a = (torch.randint(-30, 31, (n,), generator=g).float() / 30).to(torch.float16).float().abs().numpy()
+    elif kind == "bf16":
+        a = (torch.randn(n, generator=g) * 1e6).to(torch.bfloat16).float().abs().numpy()
+    elif kind == "f32":
+        a = torch.randn(n, generator=g).abs().numpy()
+    else:
+        a = torch.randn(n, generator=g).to(torch.float16).float().abs().numpy()
+    keep = _prefix_filter(a, k)
+    ci, cv = np.nonzero(keep)[0], a[keep]
+    rc, oi, ov = _select(lib, ci, cv, n, k)
+    assert rc == 0
+    assert float(np.partition(cv, cv.shape[0] - k)[cv.shape[0] - k]) == float(ov.min())
+    assert float(ov.min()) == float(np.sort(a)[n - k])
+
+
 def test_topk_select_rejects_bad_stream():
     L, lib = _lib()
     a = np.random.default_rng(1).random(10000).astype(np.float32)
