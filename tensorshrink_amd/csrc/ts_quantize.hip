@@ -25,6 +25,7 @@ constexpr int HBITS = 12;            // histogram bins on |w| float bits [30:19]
 constexpr int HBINS = 1 << HBITS;
 constexpr int HSHIFT = 31 - HBITS;
 constexpr int CHUNK = 4096;          // elements per workgroup in the scans
+constexpr int HCHUNK = 16 * CHUNK;   // elements per workgroup in the histogram pass
 
 TS_DEV float load_w(const void* w, int dt, int64_t i) {
   if (dt == TS_F16) return ts_h2f(static_cast<const uint16_t*>(w)[i]);
@@ -89,12 +90,14 @@ TS_DEV uint32_t abs_bits(const void* w, int dt, int64_t i) {
   return __builtin_bit_cast(uint32_t, load_w(w, dt, i)) & 0x7fffffffu;
 }
 
-// Per-segment histograms of |w|. A chunk touches few segments; the common
-// ones go through an LDS histogram, the rest straight to global atomics.
+// Per-segment histograms of |w|. A chunk touches few segments; the first two
+// go through an LDS histogram, the rest straight to global atomics. Chunks of
+// HCHUNK elements: clearing and flushing the 2 x HBINS LDS bins costs about
+// as much as 4096 elements' counting, so a workgroup counts 64 K of them.
 __global__ __launch_bounds__(256) void topk_hist_kernel(const void* w, int dt, int64_t n, int64_t k, uint32_t* hist) {
   __shared__ uint32_t lh[2][HBINS];
-  const int64_t c0 = (int64_t)blockIdx.x * CHUNK;
-  const int64_t c1 = min(c0 + (int64_t)CHUNK, n);
+  const int64_t c0 = (int64_t)blockIdx.x * HCHUNK;
+  const int64_t c1 = min(c0 + (int64_t)HCHUNK, n);
   const int s0 = seg_of(c0, k);
   const int64_t e0 = seg_end(s0, k);
   for (int i = threadIdx.x; i < 2 * HBINS; i += blockDim.x) (&lh[0][0])[i] = 0;
@@ -236,7 +239,7 @@ int topk_count(const ts_qinput* in, int64_t k, void* ws, size_t ws_bytes, int64_
   TopkWS t = carve_topk(ws, n, k);
   hipLaunchKernelGGL(fill_u32_kernel, dim3(256), dim3(256), 0, st, t.hist, (int64_t)t.S * HBINS, 0u);
   TS_CHECK_LAUNCH();
-  hipLaunchKernelGGL(topk_hist_kernel, dim3((unsigned)t.n_chunks), dim3(256), 0, st, in->w, in->w_dtype, n, k,
+  hipLaunchKernelGGL(topk_hist_kernel, dim3((unsigned)ts_cdiv(n, HCHUNK)), dim3(256), 0, st, in->w, in->w_dtype, n, k,
                      t.hist);
   TS_CHECK_LAUNCH();
   hipLaunchKernelGGL(topk_thr_kernel, dim3(1), dim3(256), 0, st, t.hist, t.S, k, t.thr);
