@@ -81,6 +81,13 @@ typedef struct {
    * arguments instead of reading them from device memory, where that read
    * would queue behind the layer's weight stream. NULL: read `codebook`. */
   const float* codebook_host;
+  /* Outliers of each row in column order (derived from the row-sorted tables
+   * by ts_build_colsorted_outliers; no counterpart in the reference): entry k
+   * of row r's CSR range [outlier_row_ptr[r], outlier_row_ptr[r + 1]) is
+   * col | f16 delta bits << 16, ascending in col. The prefill kernel walks a
+   * row's outliers with it while it dequantizes the row; without it (and
+   * with outliers) the forward above 16 rows runs the generic kernel. */
+  const uint32_t* outlier_colsorted;
 } ts_qlayer;
 
 const char* ts_status_str(int status);
@@ -160,6 +167,12 @@ int ts_outlier_row_ptr(const int32_t* outlier_row, int64_t n_outliers, int64_t r
 int ts_tile_outlier_max(const int32_t* outlier_row_ptr, int64_t rows, int32_t* max_count, void* stream);
 int ts_build_tile_outliers(const int32_t* outlier_row_ptr, const int32_t* outlier_row, const int32_t* outlier_col,
                            const uint16_t* outlier_delta, int64_t rows, int64_t cap, uint64_t* slots, void* stream);
+
+/* ts_qlayer.outlier_colsorted from the row-sorted CSR tables: each row's
+ * entries (col | f16 delta << 16) sorted by column. out: u32 [n_outliers].
+ * Needs every column below 65535. */
+int ts_build_colsorted_outliers(const int32_t* outlier_row_ptr, const int32_t* outlier_col,
+                                const uint16_t* outlier_delta, int64_t rows, uint32_t* out, void* stream);
 
 /*
  * QuantLinear construction (modules.py:414-448, 649-715): from codec-order

@@ -39,6 +39,7 @@ class QLayer(ctypes.Structure):
         ("outlier_row_ptr", c_vp),
         ("stage2_packed", c_vp), ("stage2_stride", c_i64), ("stage2_scale", c_vp), ("stage2_gmin", c_vp),
         ("tile_outliers", c_vp), ("tile_outlier_cap", c_i64), ("codebook_host", c_vp),
+        ("outlier_colsorted", c_vp),
     ]
 
 
@@ -71,6 +72,7 @@ PROTOTYPES = {
     "ts_outlier_tables_workspace_bytes": (c_sz, [c_i64, c_i64]),
     "ts_tile_outlier_max": (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp]),
     "ts_build_tile_outliers": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
+    "ts_build_colsorted_outliers": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
     "ts_build_outlier_tables": (ctypes.c_int, [ctypes.POINTER(QLayer), c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp,
                                                c_vp, c_sz, c_vp]),
     "ts_topk_workspace_bytes": (c_sz, [c_i64, c_i64]),

@@ -70,8 +70,20 @@ def flags() -> list:
     ]
 
 
+def _stale(src: str, obj: str) -> bool:
+    """Object older than its source or any header (TS_BUILD_INCREMENTAL=1 only)."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, h) for h in os.listdir(CSRC) if h.endswith(".h")]
+    deps.append(os.path.join(HERE, "..", "include", "tensorshrink_hip.h"))
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+    if os.environ.get("TS_BUILD_INCREMENTAL") == "1" and not _stale(src, obj):
+        return obj
     cmd = [hipcc(), *flags(), "-c", os.path.join(CSRC, src), "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

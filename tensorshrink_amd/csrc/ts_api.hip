@@ -28,6 +28,8 @@ int outlier_row_ptr(const int32_t* row, int64_t n, int64_t rows, int32_t* row_pt
 int tile_outlier_max(const int32_t* rp, int64_t rows, int32_t* out, hipStream_t st);
 int build_tile_outliers(const int32_t* rp, const int32_t* orow, const int32_t* ocol, const uint16_t* odelta,
                         int64_t rows, int64_t cap, uint64_t* slots, hipStream_t st);
+int build_colsorted_outliers(const int32_t* rp, const int32_t* ocol, const uint16_t* odelta, int64_t rows,
+                             uint32_t* out, hipStream_t st);
 size_t outlier_tables_ws(int64_t n);
 int build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n, int32_t* orow,
                          int32_t* ocol, uint16_t* odelta, int32_t* row_ptr, void* ws, size_t ws_bytes,
@@ -168,6 +170,12 @@ int ts_build_tile_outliers(const int32_t* row_ptr, const int32_t* orow, const in
                            int64_t rows, int64_t cap, uint64_t* slots, void* stream) {
   if (!row_ptr || !orow || !ocol || !odelta || !slots || rows <= 0 || cap <= 0) return TS_BAD_ARG;
   return ts::build_tile_outliers(row_ptr, orow, ocol, odelta, rows, cap, slots, S(stream));
+}
+
+int ts_build_colsorted_outliers(const int32_t* row_ptr, const int32_t* ocol, const uint16_t* odelta, int64_t rows,
+                                uint32_t* out, void* stream) {
+  if (!row_ptr || !ocol || !odelta || !out || rows < 0) return TS_BAD_ARG;
+  return ts::build_colsorted_outliers(row_ptr, ocol, odelta, rows, out, S(stream));
 }
 
 int ts_build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n, int32_t* orow,

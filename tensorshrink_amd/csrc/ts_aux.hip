@@ -444,6 +444,35 @@ __global__ __launch_bounds__(256) void tile_slots_kernel(const int32_t* __restri
   }
 }
 
+// One thread per row: the row's entries as col | delta << 16, insertion-sorted
+// by column (rows hold a handful of outliers at the configured fractions).
+__global__ __launch_bounds__(256) void colsorted_kernel(const int32_t* __restrict__ rp,
+                                                        const int32_t* __restrict__ ocol,
+                                                        const uint16_t* __restrict__ odelta, int64_t rows,
+                                                        uint32_t* __restrict__ out) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int32_t k0 = rp[r], k1 = rp[r + 1];
+  for (int32_t k = k0; k < k1; ++k) {
+    const uint32_t e = ((uint32_t)ocol[k] & 0xffffu) | ((uint32_t)odelta[k] << 16);
+    int32_t j = k;
+    while (j > k0 && (out[j - 1] & 0xffffu) > (e & 0xffffu)) {
+      out[j] = out[j - 1];
+      --j;
+    }
+    out[j] = e;
+  }
+}
+
+int build_colsorted_outliers(const int32_t* rp, const int32_t* ocol, const uint16_t* odelta, int64_t rows,
+                             uint32_t* out, hipStream_t st) {
+  if (rows <= 0) return TS_OK;
+  hipLaunchKernelGGL(colsorted_kernel, dim3((unsigned)ts_cdiv(rows, 256)), dim3(256), 0, st, rp, ocol, odelta, rows,
+                     out);
+  TS_CHECK_LAUNCH();
+  return TS_OK;
+}
+
 int tile_outlier_max(const int32_t* rp, int64_t rows, int32_t* out, hipStream_t st) {
   hipLaunchKernelGGL(tile_max_kernel, dim3(1), dim3(1024), 0, st, rp, rows, out);
   TS_CHECK_LAUNCH();

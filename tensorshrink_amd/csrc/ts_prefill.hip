@@ -7,7 +7,12 @@ namespace ts {
 int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
                     int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st) {
   if (L->padded_cols % PF_BK != 0) return TS_NOT_COVERED;
-  if (L->n_outliers > 0 && L->cols > 65535) return TS_NOT_COVERED;  // staged outlier columns are 16-bit
+  const bool has_out = L->n_outliers > 0;
+  // Outliers are walked per row in column order with 16-bit columns; the walk
+  // stops at column 0xffff, which must lie past the last k-step's end.
+  if (has_out && (L->outlier_colsorted == nullptr || L->outlier_row_ptr == nullptr ||
+                  L->padded_cols + 2 * PF_BK > (int64_t)PF_NO_COL))
+    return TS_NOT_COVERED;
   PrefillArgs a{};
   a.packed = L->packed;
   a.pstride = L->packed_stride;
@@ -29,11 +34,10 @@ int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ld
   a.s2stride = L->stage2_stride;
   a.s2scale = L->stage2_scale;
   a.s2gmin = L->stage2_gmin;
-  const bool has_out = L->n_outliers > 0 && L->outlier_row_ptr != nullptr;
+  a.has_out = has_out ? 1 : 0;
   a.orow_ptr = has_out ? L->outlier_row_ptr : static_cast<const int32_t*>(dummy);
-  a.rp_mul = has_out ? 1 : 0;
-  a.ocol = has_out ? L->outlier_col : static_cast<const int32_t*>(dummy);
-  a.odelta = has_out ? L->outlier_delta : static_cast<const uint16_t*>(dummy);
+  a.ocs = has_out ? L->outlier_colsorted : static_cast<const uint32_t*>(dummy);
+  a.ocs_bytes = has_out ? (uint32_t)(L->n_outliers * 4) : 4u;
   a.x = x;
   a.ldx = ldx;
   a.y = y;
@@ -53,7 +57,8 @@ int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ld
   const int64_t dqm = L->dq_scale_codes ? ts_cdiv(meta, L->dq_group_size) * 4 : 0;
   const int64_t s2 = L->stage2_packed ? (L->rows - 1) * L->stage2_stride + L->padded_cols / 4 : 0;
   constexpr int64_t lim = int64_t(1) << 31;
-  if (x_bytes >= lim || p_bytes >= lim || 2 * meta >= lim || dqm >= lim || s2 >= lim) return TS_NOT_COVERED;
+  if (x_bytes >= lim || p_bytes >= lim || 2 * meta >= lim || dqm >= lim || s2 >= lim || 4 * L->n_outliers >= lim)
+    return TS_NOT_COVERED;
   a.x_bytes = (uint32_t)x_bytes;
   a.p_bytes = (uint32_t)p_bytes;
   a.meta_elems = (uint32_t)meta;

@@ -48,6 +48,34 @@ def tile_outlier_slots(row_ptr: torch.Tensor, outlier_row: torch.Tensor, outlier
     return slots, cap
 
 
+# Derived outlier tables per set of outlier buffers, so that repeated calls
+# with the same QuantLinear-style buffers neither rebuild them nor sync the
+# host (the first call builds them; later calls, including ones under graph
+# capture, reuse them). Keyed on the buffers' storage and version.
+_DERIVED: dict = {}
+_DERIVED_MAX = 256
+
+
+def _derived_outliers(outlier_row, outlier_col, outlier_delta, rows: int, need_slots: bool):
+    key = (outlier_row.device.index, outlier_row.data_ptr(), outlier_row.numel(), outlier_row._version,
+           outlier_col.data_ptr(), outlier_col._version, outlier_delta.data_ptr(), outlier_delta._version, rows)
+    ent = _DERIVED.get(key)
+    if ent is None:
+        if len(_DERIVED) >= _DERIVED_MAX:
+            _DERIVED.pop(next(iter(_DERIVED)))
+        dev = outlier_row.device
+        rp = _row_ptr(outlier_row, rows)
+        ocs = torch.empty(outlier_row.numel(), dtype=torch.int32, device=dev)
+        L.check(L.lib().ts_build_colsorted_outliers(rp.data_ptr(), outlier_col.data_ptr(), outlier_delta.data_ptr(),
+                                                    rows, ocs.data_ptr(), L.stream_ptr(dev)), "column-sorted outliers")
+        ent = {"rp": rp, "ocs": ocs, "slots": None, "cap": 0,
+               "keep": (outlier_row, outlier_col, outlier_delta)}
+        _DERIVED[key] = ent
+    if need_slots and ent["slots"] is None:
+        ent["slots"], ent["cap"] = tile_outlier_slots(ent["rp"], outlier_row, outlier_col, outlier_delta, rows)
+    return ent
+
+
 def fused_quantized_linear(
     x: torch.Tensor, packed: torch.Tensor, scale: Optional[torch.Tensor], gmin: Optional[torch.Tensor],
     bias: Optional[torch.Tensor], bits: int, group_size: int, cols: int, out_features: int,
@@ -90,15 +118,15 @@ def fused_quantized_linear(
     if stage2_packed is not None:
         s.stage2_packed, s.stage2_stride = stage2_packed.data_ptr(), stage2_packed.shape[1]
         s.stage2_scale, s.stage2_gmin = stage2_scale.data_ptr(), stage2_gmin.data_ptr()
-    rp = slots = None
     if outlier_row is not None and outlier_row.numel() > 0:
-        rp = _row_ptr(outlier_row, out_features)
+        ent = _derived_outliers(outlier_row, outlier_col, outlier_delta, out_features, need_slots=M <= 16)
         s.outlier_row, s.outlier_col = outlier_row.data_ptr(), outlier_col.data_ptr()
         s.outlier_delta, s.n_outliers = outlier_delta.data_ptr(), outlier_row.numel()
-        s.outlier_row_ptr = rp.data_ptr()
-        if M <= 16:  # the decode kernel reads outliers per tile
-            slots, cap = tile_outlier_slots(rp, outlier_row, outlier_col, outlier_delta, out_features)
-            s.tile_outliers, s.tile_outlier_cap = slots.data_ptr(), cap
+        s.outlier_row_ptr = ent["rp"].data_ptr()
+        if s.padded_cols < 65535:
+            s.outlier_colsorted = ent["ocs"].data_ptr()
+        if ent["slots"] is not None:  # the decode kernel reads outliers per tile
+            s.tile_outliers, s.tile_outlier_cap = ent["slots"].data_ptr(), ent["cap"]
     ydt = torch.float32 if return_fp32 else compute_dtype
     if out is None or out.shape != (M, out_features) or out.dtype != ydt or not out.is_contiguous():
         out = torch.empty(M, out_features, dtype=ydt, device=x.device)
@@ -122,7 +150,7 @@ def apply_outlier_correction(out: torch.Tensor, x2d: torch.Tensor, outlier_row: 
         return out
     out2d = out.reshape(-1, out.shape[-1])
     rows = out2d.shape[1]
-    rp = _row_ptr(outlier_row, rows)
+    rp = _derived_outliers(outlier_row, outlier_col, outlier_delta, rows, need_slots=False)["rp"]
     x2d = x2d.contiguous()
     L.check(L.lib().ts_apply_outlier_correction(out2d.data_ptr(), out2d.shape[0], out2d.stride(0), x2d.data_ptr(),
                                                 x2d.stride(0), L.dtype_code(x2d.dtype), rp.data_ptr(),

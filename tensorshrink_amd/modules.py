@@ -14,6 +14,9 @@ Additions over the reference:
   * ``tile_outliers`` - non-persistent per-16-row-tile outlier slots (u64:
     col, row in tile, f16 delta; ``tile_outlier_cap`` slots per tile) that
     the decode kernel reads at a fixed address (derived data);
+  * ``outlier_colsorted`` - non-persistent per-row column-sorted outliers
+    (u32: col | f16 delta << 16) that the prefill kernel walks while it
+    dequantizes a row (derived data);
   * 6-bit RVQ layers register ``stage2_packed``, ``stage2_scale`` and
     ``stage2_gmin`` (the reference QuantLinear cannot serve bits=6).
 ``WeightCache`` (a dense-weight cache) is not part of this path: passing
@@ -135,6 +138,14 @@ class QuantLinear(nn.Module):
         else:
             slots, self.tile_outlier_cap = torch.zeros(0, dtype=torch.int64, device=dev), 0
         self.register_buffer("tile_outliers", slots, persistent=False)
+        # derived column-sorted copy per row for the prefill kernel
+        ocs = torch.empty(n, dtype=torch.int32, device=dev)
+        if n > 0:
+            with torch.cuda.device(dev):
+                L.check(lib.ts_build_colsorted_outliers(rptr.data_ptr(), ocol.data_ptr(), odelta.data_ptr(),
+                                                        self.rows, ocs.data_ptr(), L.stream_ptr(dev)),
+                        "column-sorted outliers")
+        self.register_buffer("outlier_colsorted", ocs, persistent=False)
         if bias is not None:
             self.register_buffer("bias", bias.detach().clone().to(dev))
         else:
@@ -178,14 +189,31 @@ class QuantLinear(nn.Module):
             if self.tile_outlier_cap > 0:
                 s.tile_outliers = self.tile_outliers.data_ptr()
                 s.tile_outlier_cap = self.tile_outlier_cap
+            if self.padded_cols < 65535:
+                s.outlier_colsorted = self.outlier_colsorted.data_ptr()
         return s
 
     def _rebuild_cache(self) -> None:
         self._layer = self._make_layer() if self.packed.is_cuda else None
         self._bias_cache = {}
 
+    # Buffers the kernels read with a fixed element type. Module-wide casts
+    # (`.half()`, `.to(torch.bfloat16)`) convert every floating buffer; these
+    # are cast back so the kernel view keeps reading them as it expects (the
+    # reference casts its metadata to float32 where it uses it, so the same
+    # flow works there).
+    _FIXED_DTYPES = {
+        "scale": torch.float16, "gmin": torch.float16, "dq_scale_meta": torch.float16,
+        "dq_gmin_meta": torch.float16, "codebook": torch.float32, "outlier_delta": torch.float16,
+        "stage2_scale": torch.float16, "stage2_gmin": torch.float16,
+    }
+
     def _apply(self, fn, recurse=True):
         result = super()._apply(fn, recurse=recurse)
+        for name, dt in self._FIXED_DTYPES.items():
+            b = self._buffers.get(name)
+            if b is not None and b.dtype != dt:
+                self._buffers[name] = b.to(dt)
         self._rebuild_cache()
         return result
 
@@ -291,12 +319,12 @@ class QuantLinear(nn.Module):
         b = self._bias_as(in_dtype)
         dt = L.dtype_code(in_dtype)
         lib = L.load()
-        # large M: room for the dequantized layer + GEMM (0 below the threshold)
-        ws_n = lib.ts_forward_workspace_bytes(ctypes.byref(self._layer), M)
-        ws = torch.empty(ws_n, dtype=torch.uint8, device=x.device) if ws_n else None
-        L.check(lib.ts_qlinear_forward(ctypes.byref(self._layer), x2d.data_ptr(), M, self.in_features, dt,
-                                       y.data_ptr(), self.out_features, dt, L.ptr(b), L.ptr(ws), ws_n,
-                                       L.stream_ptr(x.device)), "qlinear forward")
+        # no workspace: M <= 16 runs the decode kernel, larger M the fused
+        # dequant-into-LDS MFMA kernel
+        with torch.cuda.device(x.device):
+            L.check(lib.ts_qlinear_forward(ctypes.byref(self._layer), x2d.data_ptr(), M, self.in_features, dt,
+                                           y.data_ptr(), self.out_features, dt, L.ptr(b), None, 0,
+                                           L.stream_ptr(x.device)), "qlinear forward")
         return y.reshape(*lead, self.out_features)
 
     @staticmethod
@@ -327,8 +355,9 @@ class QuantLinear(nn.Module):
             ld = (ctypes.c_int64 * n)(*[q.out_features for q in layers])
             bp = (ctypes.c_void_p * n)(*[L.ptr(b) for b in bs])
             dt = L.dtype_code(in_dtype)
-            rc = L.load().ts_qlinear_forward_group(qls, n, x2d.data_ptr(), M, layers[0].in_features, dt, yp, ld, dt,
-                                                   bp, L.stream_ptr(x.device))
+            with torch.cuda.device(x.device):
+                rc = L.load().ts_qlinear_forward_group(qls, n, x2d.data_ptr(), M, layers[0].in_features, dt, yp, ld,
+                                                       dt, bp, L.stream_ptr(x.device))
             if rc != L.TS_NOT_COVERED:
                 L.check(rc, "qlinear group forward")
                 return [y.reshape(*lead, q.out_features) for y, q in zip(ys, layers)]

@@ -137,7 +137,36 @@ LARGE_CASES = [
          frac=0.001),
     dict(name="cfg5_nf4_dq_28672x8192", kind="gauss", rows=28672, cols=8192, seed=5004, sigma=0.015, bits=4,
          gs=128, frac=0.001, dq=True, nf=True),
+    dict(name="cfg2_lm2_g64_11008x4096", kind="student", rows=11008, cols=4096, seed=2000, bits=2, gs=64,
+         frac=0.001, lm=True, manual_seed=2024),
 ]
+# Every other layer the config-scale forward tests use, so that each one's
+# reference weight (dequantize_tensor) is pinned by a digest.
+_NF4 = dict(bits=4, gs=128, frac=0.001, dq=True, nf=True)
+_NF8 = dict(bits=8, gs=128, frac=0.001, dq=True, nf=True)
+_RVQ6 = dict(bits=6, gs=128, frac=0.001, dq=True)
+_LLAMA8B = dict(q=(4096, 4096), k=(1024, 4096), v=(1024, 4096), o=(4096, 4096), gate=(14336, 4096),
+                up=(14336, 4096), down=(4096, 14336))
+_LLAMA70B = dict(q=(8192, 8192), k=(1024, 8192), v=(1024, 8192), o=(8192, 8192), gate=(28672, 8192),
+                 up=(28672, 8192), down=(8192, 28672))
+# BASELINE config 5's bit-width mix: attention 8-bit, MLP 4-bit, down 2-bit companded
+_CFG5 = dict(q=_NF8, k=_NF8, v=_NF8, o=_NF8, gate=_NF4, up=_NF4,
+             down=dict(bits=2, gs=64, frac=0.001, dq=True, lm=True, manual_seed=7))
+for _i, (_n, (_r, _c)) in enumerate(_LLAMA8B.items()):
+    if _i > 0:  # layer 0 (q, seed 1000) is cfg1 above
+        LARGE_CASES.append(dict(name=f"cfg3_{_n}_nf4_dq_{_r}x{_c}", kind="gauss", rows=_r, cols=_c, seed=1000 + _i,
+                                **_NF4))
+for _i, _n in ((4, "gate"), (5, "up"), (6, "down")):
+    _r, _c = _LLAMA8B[_n]
+    if _i != 4:
+        LARGE_CASES.append(dict(name=f"cfg4_{_n}_nf8_dq_{_r}x{_c}", kind="gauss", rows=_r, cols=_c, seed=1000 + _i,
+                                **_NF8))
+    if _i != 5:
+        LARGE_CASES.append(dict(name=f"cfg4_{_n}_rvq6_dq_{_r}x{_c}", kind="gauss", rows=_r, cols=_c,
+                                seed=1000 + _i, **_RVQ6))
+for _i, (_n, (_r, _c)) in enumerate(_LLAMA70B.items()):
+    LARGE_CASES.append(dict(name=f"cfg5_{_n}_{_r}x{_c}", kind="gauss", rows=_r, cols=_c, seed=5100 + _i,
+                            sigma=0.015, **_CFG5[_n]))
 
 
 def run_case(codec, modules, spec: dict, full: bool):
@@ -205,7 +234,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--small", action="store_true")
     ap.add_argument("--large", action="store_true")
-    ap.add_argument("--only", default=None)
+    ap.add_argument("--only", default=None, help="comma-separated case names")
+    ap.add_argument("--missing", action="store_true", help="large cases without a digest yet")
     args = ap.parse_args()
     if not (args.small or args.large):
         args.small = True
@@ -235,8 +265,11 @@ def main():
     if args.large:
         path = os.path.join(HERE, "digests.json")
         dig = json.load(open(path)) if os.path.exists(path) else {}
+        only = set(args.only.split(",")) if args.only else None
         for spec in LARGE_CASES:
-            if args.only and spec["name"] != args.only:
+            if only and spec["name"] not in only:
+                continue
+            if args.missing and spec["name"] in dig:
                 continue
             t0 = time.time()
             res, _ = run_case(codec, modules, spec, full=False)

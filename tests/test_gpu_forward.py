@@ -67,21 +67,60 @@ def test_forward_fp32_and_3d_input():
     assert max_rel_err(y.cpu().reshape(6, -1), y_ref) <= TOL
 
 
+def _oracle_opts(opts):
+    return dict(bits=opts["bits"], group_size=opts["group_size"], outlier_frac=opts["outlier_frac"],
+                double_quant=opts.get("double_quant", False), nf_quant=opts.get("nf_quant", False))
+
+
 def _layer(rows, cols, seed, opts, sigma=0.02):
+    """QuantLinear for a seeded layer and its reference weight: the oracle's
+    dequantize_tensor of the oracle's quantize, after checking that the GPU
+    codec's arrays equal the oracle's bit for bit."""
     ts = _ts()
+    from oracle import codec_ref as O
     w = recipes.gaussian_weight(rows, cols, seed, sigma=sigma)
     qt = ts.quantize_tensor(w, **opts)
+    q_ref = O.quantize(w, **_oracle_opts(opts))
+    for f in ("packed", "outlier_idx", "outlier_val", "scale", "gmin", "dq_scale_codes", "stage2_packed"):
+        if f in q_ref:
+            np.testing.assert_array_equal(getattr(qt, f).view(np.uint8), q_ref[f].view(np.uint8), err_msg=f)
+    W = torch.from_numpy(O.dequantize(q_ref, "f32")).cuda()
+    return ts.QuantLinear(qt), W
+
+
+def _pinned(name):
+    """QuantLinear for a config-scale digest case and its reference weight:
+    the GPU codec's arrays and float32 dequantize_tensor output, each checked
+    against the reference's SHA-256 digest before use."""
+    from golden_io import digests, qopts
+    from gpu_util import sha
+    ts = _ts()
+    dig = digests()[name]
+    spec = dig["spec"]
+    w = weight_for(spec)
+    if spec.get("lm"):
+        torch.manual_seed(spec["manual_seed"])
+    qt = ts.quantize_tensor(w, **qopts(spec))
+    del w
+    for f, h in dig["digests"].items():
+        if f not in ("deq_f32", "deq_native"):
+            assert sha(getattr(qt, f)) == h, (name, f)
     W = ts.dequantize_tensor(qt, device="cuda", dtype=torch.float32)
+    assert sha(W.cpu().numpy()) == dig["digests"]["deq_f32"], name
     return ts.QuantLinear(qt), W
 
 
 NF4 = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+CFG3_NAMES = ["cfg1_nf4_dq_4096x4096"] + [f"cfg3_{n}_nf4_dq_{r}x{c}" for n, r, c in recipes.LLAMA3_8B_LINEARS[1:]]
+CFG4_NAMES = {8: ["cfg4_nf8_dq_14336x4096", "cfg4_up_nf8_dq_14336x4096", "cfg4_down_nf8_dq_4096x14336"],
+              6: ["cfg4_gate_rvq6_dq_14336x4096", "cfg4_rvq6_dq_14336x4096", "cfg4_down_rvq6_dq_4096x14336"]}
+CFG5_NAMES = [f"cfg5_{n}_{r}x{c}" for n, r, c in recipes.LLAMA3_70B_LINEARS]
 
 
 @pytest.mark.slow
 @pytest.mark.parametrize("M", [1, 16])
 def test_cfg1_4096_nf4(M):
-    ql, W = _layer(4096, 4096, 1000, NF4)
+    ql, W = _pinned("cfg1_nf4_dq_4096x4096")
     x = recipes.activations(M, 4096).cuda()
     err = max_rel_err(ql(x).float(), x.float() @ W.T)
     say("cfg1 M", M, "err", err)
@@ -89,38 +128,36 @@ def test_cfg1_4096_nf4(M):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("M", [1, 4, 8])
-def test_cfg2_11008_lm2(M):
-    ts = _ts()
-    w = recipes.student_t_weight(11008, 4096, 2000)
-    torch.manual_seed(2024)
-    qt = ts.quantize_tensor(w, bits=2, group_size=64, outlier_frac=0.001, double_quant=True, companded=True)
-    W = ts.dequantize_tensor(qt, device="cuda", dtype=torch.float32)
-    ql = ts.QuantLinear(qt)
-    x = recipes.activations(M, 4096).cuda()
-    err = max_rel_err(ql(x).float(), x.float() @ W.T)
-    say("cfg2 M", M, "err", err)
-    assert err <= TOL
+@pytest.mark.parametrize("name", ["cfg2_lm2_dq_11008x4096", "cfg2_lm2_g64_11008x4096"])
+def test_cfg2_11008_lm2(name):
+    """2-bit Lloyd-Max, group 64, with and without double quant."""
+    ql, W = _pinned(name)
+    for M in (1, 4, 8):
+        x = recipes.activations(M, 4096).cuda()
+        err = max_rel_err(ql(x).float(), x.float() @ W.T)
+        say("cfg2", name, M, err)
+        assert err <= TOL, (M, err)
 
 
 @pytest.mark.slow
 def test_cfg3_llama8b_layer():
-    for i, (name, n, k) in enumerate(recipes.LLAMA3_8B_LINEARS):
-        ql, W = _layer(n, k, recipes.layer_seed(i), NF4)
+    for name, (lname, n, k) in zip(CFG3_NAMES, recipes.LLAMA3_8B_LINEARS):
+        ql, W = _pinned(name)
         for M in (1, 4, 16):
             x = recipes.activations(M, k).cuda()
             err = max_rel_err(ql(x).float(), x.float() @ W.T)
-            say("cfg3", name, M, err)
-            assert err <= TOL, (name, M, err)
+            say("cfg3", lname, M, err)
+            assert err <= TOL, (lname, M, err)
         del ql, W
         torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("bits,frac", [(4, 0.05), (8, 0.03), (6, 0.02)])
 def test_forward_dense_outliers(bits, frac):
-    """Rows with more outliers than the prefill kernel stages per tile row
-    (their rest is added in the epilogue) and more than the decode kernel's
-    default slot count."""
+    """Rows with many outliers (about 100 per row at 5 %, several in one
+    64-column k-step of a row): the decode kernel's tile slots and the
+    prefill kernel's per-row walk, through QuantLinear and the C-ABI without
+    a workspace."""
     opts = dict(bits=bits, group_size=128, outlier_frac=frac, double_quant=True, nf_quant=bits != 6)
     ql, W = _layer(256, 2048, 31 + bits, opts)
     for M in (1, 16, 64, 300):
@@ -128,48 +165,66 @@ def test_forward_dense_outliers(bits, frac):
         err = max_rel_err(ql(x).float(), x.float() @ W.T)
         say("dense outliers", bits, frac, M, err)
         assert err <= TOL, (M, err)
+        if M > 16:
+            err = max_rel_err(_forward_no_workspace(ql, x).float(), x.float() @ W.T)
+            assert err <= TOL, ("fused", M, err)
+
+
+def test_forward_outliers_in_one_row():
+    """Every outlier of the layer in one row (the decode tile slots of one
+    tile and the prefill walk of one thread take them all), at decode and
+    prefill sizes."""
+    ts = _ts()
+    from oracle import codec_ref as O
+    w = recipes.gaussian_weight(512, 1024, 55, outlier_frac=0.0)
+    w[300, ::2] = (torch.arange(512, dtype=torch.float32) % 7 + 3).to(w.dtype)  # 512 large values in row 300
+    opts = dict(bits=4, group_size=128, outlier_frac=512 / (512 * 1024), double_quant=True, nf_quant=True)
+    qt = ts.quantize_tensor(w, **opts)
+    q_ref = O.quantize(w, **_oracle_opts(opts))
+    np.testing.assert_array_equal(qt.outlier_idx, q_ref["outlier_idx"])
+    assert (qt.outlier_idx // 1024 == 300).all()
+    ql = ts.QuantLinear(qt)
+    W = torch.from_numpy(O.dequantize(q_ref, "f32")).cuda()
+    for M in (1, 7, 16, 33, 260):
+        x = recipes.activations(M, 1024, seed=M).cuda()
+        err = max_rel_err(ql(x).float(), x.float() @ W.T)
+        say("one-row outliers", M, err)
+        assert err <= TOL, (M, err)
 
 
 @pytest.mark.slow
 @pytest.mark.parametrize("bits", [8, 6])
-def test_cfg4_prefill_2048(bits):
-    opts = dict(bits=bits, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
-    x = recipes.activations(2048, 4096).cuda()
-    for i, (name, n, k) in enumerate(recipes.LLAMA3_8B_LINEARS[4:6]):
-        ql, W = _layer(n, k, recipes.layer_seed(4 + i), opts)
-        err = max_rel_err(ql(x).float(), x.float() @ W.T)
-        say("cfg4", bits, name, err)
-        assert err <= TOL
-    name, n, k = recipes.LLAMA3_8B_LINEARS[6]
-    ql, W = _layer(n, k, recipes.layer_seed(6), opts)
-    x2 = recipes.activations(2048, k).cuda()
-    err = max_rel_err(ql(x2).float(), x2.float() @ W.T)
-    say("cfg4", bits, name, err)
-    assert err <= TOL
-
-
-# the 70B layer's adaptive mix (attention 8-bit, MLP 4-bit,
-# down 2-bit companded), fp16 N(0, 0.015) weights with outliers.
-CFG5_OPTS = {
-    "q": dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True),
-    "k": dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True),
-    "v": dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True),
-    "o": dict(bits=8, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True),
-    "gate": NF4, "up": NF4,
-    "down": dict(bits=2, group_size=64, outlier_frac=0.001, double_quant=True, companded=True),
-}
+@pytest.mark.parametrize("layer", [0, 1, 2])
+def test_cfg4_prefill_2048(bits, layer):
+    """the fused dequant-into-LDS MFMA kernel (QuantLinear's
+    path above 16 rows) on the Llama-3-8B gate/up/down at M = 2048, 8-bit NF8
+    + double quant and 6-bit RVQ, against x @ W^T with the digest-pinned W.
+    Also the dequantize + library GEMM path (a workspace passed through the
+    C-ABI) on the same layer."""
+    name = CFG4_NAMES[bits][layer]
+    ql, W = _pinned(name)
+    x = recipes.activations(2048, ql.in_features).cuda()
+    ref = x.float() @ W.T
+    y = ql(x)
+    err = max_rel_err(y.float(), ref)
+    say("cfg4", bits, name, "fused", err)
+    assert err <= TOL, err
+    err_g = max_rel_err(_forward_gemm(ql, x).float(), ref)
+    say("cfg4", bits, name, "dequant+gemm", err_g)
+    assert err_g <= TOL, err_g
 
 
 @pytest.mark.slow
 def test_cfg5_llama70b_layer_decode():
-    torch.manual_seed(7)
-    for i, (name, n, k) in enumerate(recipes.LLAMA3_70B_LINEARS):
-        ql, W = _layer(n, k, 5100 + i, CFG5_OPTS[name], sigma=0.015)
+    """BASELINE config 5's layer (8-bit attention, 4-bit MLP, 2-bit companded
+    down) at decode sizes against the digest-pinned weights."""
+    for name, (lname, n, k) in zip(CFG5_NAMES, recipes.LLAMA3_70B_LINEARS):
+        ql, W = _pinned(name)
         for M in (1, 4, 16):
             x = recipes.activations(M, k, seed=M).cuda()
             err = max_rel_err(ql(x).float(), x.float() @ W.T)
-            say("cfg5", name, M, err)
-            assert err <= TOL, (name, M, err)
+            say("cfg5", lname, M, err)
+            assert err <= TOL, (lname, M, err)
         del ql, W
         torch.cuda.empty_cache()
 
@@ -237,6 +292,21 @@ def test_forward_group_fallbacks():
         assert max_rel_err(yb.float(), x.float() @ Wb.T) <= TOL
 
 
+def _forward_gemm(ql, x):
+    """ts_qlinear_forward with a workspace: dequantize + one library GEMM."""
+    from tensorshrink_amd import _lib as L
+    y = torch.empty(x.shape[0], ql.out_features, dtype=x.dtype, device=x.device)
+    b = None if ql.bias is None else ql.bias.to(x.dtype).contiguous()
+    lib = L.load()
+    n = lib.ts_forward_workspace_bytes(ctypes.byref(ql._layer), x.shape[0])
+    ws = torch.empty(n, dtype=torch.uint8, device=x.device)
+    dt = L.dtype_code(x.dtype)
+    L.check(lib.ts_qlinear_forward(ctypes.byref(ql._layer), x.data_ptr(), x.shape[0], ql.in_features, dt,
+                                   y.data_ptr(), ql.out_features, dt, L.ptr(b), ws.data_ptr(), n, L.stream_ptr()),
+            "fwd gemm")
+    return y
+
+
 def _forward_no_workspace(ql, x):
     """ts_qlinear_forward without a workspace: the fused MFMA prefill kernel."""
     import ctypes
@@ -279,8 +349,7 @@ def test_dequantize_weight_vector_pass_matches_scalar(opts):
 def test_forward_graph_replay(M):
     """QuantLinear.forward captured in a HIP graph and replayed four times, with
     eager work and synchronisation between replays: every replay equals the
-    eager call (decode for M <= 16; dequantize into the workspace + hipBLASLt
-    above, the algorithm chosen by the eager call's tuning)."""
+    eager call (decode kernel for M <= 16, the fused prefill kernel above)."""
     ts = _ts()
     ql, W = _layer(1024, 2048, 77, NF4)
     ql.bias = torch.randn(ql.out_features, dtype=torch.bfloat16).cuda()
@@ -321,8 +390,8 @@ def test_forward_gemm_path(M, dtype, bias):
     assert L.load().ts_forward_workspace_bytes(__import__("ctypes").byref(ql._layer), M) >= 768 * 1536 * 2
     assert L.load().ts_forward_workspace_bytes(__import__("ctypes").byref(ql._layer), 16) == 0
     x = recipes.activations(M, 1536, seed=M, dtype=dtype).cuda()
-    y = ql(x)
-    y_fused = _forward_no_workspace(ql, x)
+    y = _forward_gemm(ql, x)
+    y_fused = ql(x)
     ref = x.float() @ W.T + (ql.bias.float() if bias else 0)
     say("gemm path", M, dtype, bias, max_rel_err(y.float(), ref), max_rel_err(y_fused.float(), ref))
     assert y.dtype == dtype
