@@ -8,37 +8,42 @@
 // the tile's outliers into it and feeds MFMA f32_32x32x16 with fp32
 // accumulation.
 //
-// Tile 256 x BN x 64 per workgroup of 4 waves, one wave per SIMD (2 x 2
-// waves, each 128 x BN/2 as 4 x BN/64 MFMA blocks of 32 x 32; the
-// accumulators live in AGPRs). Sized for gfx950's budget per CU and clock:
-// one 32x32x16 MFMA takes 32 cycles of a SIMD, and the LDS moves about 190 B
-// per cycle. A 128 x 128 wave tile reads 8 KB of operands per 16 MFMAs
-// (64 B per MFMA-cycle over the CU); with the tile stores and the codebook
-// lookups the LDS stays near 60 % of its rate, so the k-loop can run at the
-// MFMA rate. Each weight element is dequantized once per workgroup.
+// Tiles of 256 x BN x 64. BN = 256 (when the tiles fill the CUs): 8 waves,
+// two per SIMD, as a 2 x 4 grid of 128 x 64 wave tiles (4 x 2 MFMA blocks of
+// 32 x 32); BN = 128: 4 waves, one per SIMD, 2 x 2 grid of 128 x 64. Each
+// weight element is dequantized once per workgroup. Sized from gfx950
+// measurements: a 32x32x16 MFMA occupies a SIMD for 32 cycles; the LDS serves
+// ds_read_b128 at about 190 B per cycle, ds_write_b128 at half that, and a
+// 64-lane codebook lookup (ds_read_u16) costs about as much as a b128 read,
+// so NF8's 256 lookups per k-step are the largest single LDS cost.
 //   * All global reads are raw buffer loads (64-bit bases in SGPRs, 32-bit
-//     offsets) into register stages: weights two k-steps ahead, x (two
-//     register sets) two k-steps ahead. No load is conditional, so the
-//     compiler's wait counts stay exact and a wait never drains younger
-//     loads.
-//   * One k-step = 4 MFMA sub-steps over LDS buffer `cur`. The operand
-//     fragments of sub-step s + 1 are read before sub-step s's MFMAs; the next
-//     stage's dequant (codebook lookup, scale, convert, write to buffer
-//     `cur ^ 1`) and x store are spread over sub-steps 0-2. The one LDS
-//     barrier per k-step sits before sub-step 3, whose fragments are already
-//     in registers, so the next k-step's first fragment reads overlap its
-//     MFMAs.
+//     offsets) into register stages: weights two k-steps ahead, x one.
+//     No load the compiler tracks is conditional, so its wait counts stay
+//     exact and a wait never drains younger loads.
+//   * One k-step = 4 MFMA sub-steps over LDS buffer `cur` while the next
+//     stage is dequantized (codebook lookup, scale, convert) into buffer
+//     `cur ^ 1`. 8 waves: each sub-step reads its fragments just before its
+//     MFMAs and the other wave of the SIMD covers the wait; x is stored at
+//     the start of the k-step; one barrier at the end. 4 waves: fragments
+//     and codebook values are read a sub-step ahead, MFMAs are interleaved
+//     with the dequant work, and the barrier sits before sub-step 3.
 //   * LDS tiles use a 16-byte-chunk XOR swizzle (chunk c of row r at
-//     c ^ (r & 7)): tile writes and MFMA operand reads are conflict free.
-//   * Codebooks sit in LDS in bank-interleaved copies, so random code
-//     lookups spread over the banks.
-//   * Outliers: each weight row is dequantized by one thread (two for
-//     BN = 128) that walks the row's outliers in column order (a derived
+//     c ^ (r & 7) ^ ((r >> 3) & 1)): MFMA operand reads are conflict free on
+//     gfx950's 64-bank LDS.
+//   * Codebooks sit in LDS as f16 values in 32 bank-interleaved copies (one
+//     32-bit slot each; lane l reads copy l % 32, in bank l % 32), so random
+//     code lookups are conflict free, and each value feeds a mixed-precision
+//     FMA (v_fma_mix_f32) directly. f16 keeps the NF8 grid (values in
+//     [0, 255]) to 2^-11 relative, finer than the bf16 the reference's
+//     kernels cast it to.
+//   * Outliers: each weight row is dequantized by two threads (32 columns
+//     of a k-step each) that walk the row's outliers in column order (a derived
 //     column-sorted table) and adds each delta into the element it has just
 //     written with an LDS packed add (ds_pk_add_bf16 / _f16), i.e.
 //     w = cast(cast(w) + cast(delta)), as modules.py:918 folds them into the
 //     dense W. The next entry is loaded a k-step ahead; a second outlier of the
-//     same row in one k-step waits for its load.
+//     same row in one k-step waits for its load (a synchronous load the
+//     compiler does not track, so the common path never drains).
 #pragma once
 #include <algorithm>
 #include <mutex>
@@ -82,6 +87,9 @@ struct PrefillArgs {
 constexpr int PF_BM = 256;
 constexpr int PF_BK = 64;
 constexpr uint32_t PF_NO_COL = 0xffffu;  // column of the "no more outliers" entry
+#ifndef PF_NW_WIDE
+#define PF_NW_WIDE 8  // waves per workgroup of the 256 x 256 tile
+#endif
 
 typedef __bf16 ts_bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 ts_f16x2 __attribute__((ext_vector_type(2)));
@@ -97,8 +105,25 @@ TS_DEV uint32_t to_pair(float lo, float hi) {
   else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, ts_f16x2));
 }
 
-// LDS offset (in uint16 elements) of 16-byte chunk c of row r in a [rows][64] tile.
-TS_DEV int swz(int r, int c) { return r * PF_BK + ((c ^ (r & 7)) << 3); }
+// LDS offset (in uint16 elements) of 16-byte chunk c of row r in a [rows][64]
+// tile. gfx950 serves ds_read_b128 16 lanes at a time over 64 banks (256 B):
+// the MFMA operand reads (lanes 0-15 = rows r..r+15, one chunk column) are
+// conflict free when rows r and r + 8, which share r & 7 and the bank half
+// given by r & 1, land on different chunk positions, hence the (r >> 3) term
+// (measured: 40 % more b128 read throughput than c ^ (r & 7) alone).
+TS_DEV int swz(int r, int c) { return r * PF_BK + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 3); }
+
+// Synchronous 32-bit global load for the rare path of the outlier walk (a
+// second outlier of one row within one k-step). Issued from inline asm with
+// its own wait, so that the compiler sees no load in the branch: a load it
+// tracks inside a divergent branch makes it wait for every outstanding load
+// (vmcnt(0)) where the branches join, which drained the weight and x
+// prefetches on every k-step.
+TS_DEV uint32_t ts_load_sync(const uint32_t* p) {
+  uint32_t v;
+  asm volatile("global_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
 
 // Workgroup index -> tile index, so that the workgroups one XCD runs (the
 // hardware deals workgroups out to the 8 XCDs round robin) take consecutive
@@ -109,11 +134,12 @@ TS_DEV int64_t xcd_tile(int64_t b, int64_t n) {
   return x * q + min(x, r) + i;
 }
 
-template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN>
-__global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in) {
-  constexpr int BM = PF_BM, BK = PF_BK, NT = 256;
+template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a_in) {
+  constexpr int BM = PF_BM, BK = PF_BK, NT = 64 * NW;
+  constexpr int WN = NW / 2;                    // waves along N (two along M)
   constexpr int TM = 4;                         // 32-row blocks per wave along M (128 rows)
-  constexpr int TN = BN / 64;                   // 32-column blocks per wave along N (BN / 2)
+  constexpr int TN = BN / (32 * WN);            // 32-column blocks per wave along N
   constexpr int TPR = NT / BN;                  // threads per weight row (1 or 2)
   constexpr int CPT = BK / TPR;                 // weight codes per thread per k-step (64 or 32)
   constexpr int C8 = CPT / 8;                   // 8-code chunks per thread per k-step
@@ -123,7 +149,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
   constexpr int WW2 = RVQ ? CPT / 16 : 1;       // stage-2 dwords (16 two-bit codes each)
   constexpr int NGT = CPT > GS ? CPT / GS : 1;  // groups a thread's codes span in a k-step
   constexpr int CBN = CB ? (1 << BITS) : 1;
-  constexpr int CBC = (CB && BITS == 8) ? 16 : 32;  // codebook copies (bank spread)
+  constexpr int CBC = 32;                       // codebook copies: lane l reads copy l % 32 (bank l % 32)
   constexpr int XCH = BM * 8 / NT;              // 16-byte x chunks per thread per k-step
   static_assert(WB >= 8 && WB % 8 == 0, "packed chunk");
   static_assert(GS % BK == 0 || BK % GS == 0, "group size");
@@ -144,10 +170,10 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
 
   uint16_t* As = reinterpret_cast<uint16_t*>(smem);          // [2][BM][64]
   uint16_t* Bs = As + 2 * BM * BK;                           // [2][BN][64]
-  float* cbs = reinterpret_cast<float*>(Bs + 2 * BN * BK);   // [CBN][CBC]
+  uint32_t* cbs = reinterpret_cast<uint32_t*>(Bs + 2 * BN * BK);  // [CBN][CBC] f16 in the low half
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave & 1, wn = wave >> 1;  // wave (wm, wn) of the 2 x WN grid
   const uint32_t cb_lane = lane % CBC;
 
   const int64_t tile = xcd_tile(blockIdx.x, a.m_tiles * a.n_tiles);
@@ -182,13 +208,13 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
     uint32_t sm[NGT], gm[NGT];  // DQ (meta_scale, meta_min) f16 pairs
     uint32_t s2[NGT];           // RVQ stage-2 (scale, gmin) f16 bits
   };
-  // x: thread tid owns chunk column tid & 7 of rows tid / 8 + 32 i. Rows
+  // x: thread tid owns chunk column tid & 7 of rows tid / 8 + (NT / 8) i. Rows
   // past M and chunks whose columns lie past `cols` are read at offsets past
   // the buffer's extent (bit 31 set for the latter), which the buffer load
   // returns as zeros; those rows are never stored.
   ts_u32x4 X[XCH];
   const uint32_t xbase = (uint32_t)((m0 + (tid >> 3)) * a.ldx) * 2u + (tid & 7) * 16u;
-  const uint32_t xstep = (uint32_t)(32 * a.ldx * 2);
+  const uint32_t xstep = (uint32_t)((NT / 8) * a.ldx * 2);
   const int xcol = (tid & 7) * 8;
   auto load_x = [&](int kt, ts_u32x4* xr) {
     kt = min(kt, KT - 1);
@@ -196,7 +222,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
     const uint32_t oob = (kt * BK + xcol < a.cols) ? 0u : 0x80000000u;
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      const int64_t m = m0 + (tid >> 3) + 32 * i;
+      const int64_t m = m0 + (tid >> 3) + (NT / 8) * i;
       xr[i] = ts_bld16s(rx, (m < a.M ? xbase + i * xstep : 0x7fffffffu) | oob, kb);
     }
   };
@@ -204,7 +230,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
     uint16_t* Ab = As + buf * BM * BK;
 #pragma unroll
     for (int i = 0; i < XCH; ++i)
-      *reinterpret_cast<ts_u32x4*>(Ab + swz((tid >> 3) + 32 * i, tid & 7)) = xr[i];
+      *reinterpret_cast<ts_u32x4*>(Ab + swz((tid >> 3) + (NT / 8) * i, tid & 7)) = xr[i];
   };
   auto load_stage = [&](int kt, Stage& S) {
     kt = min(kt, KT - 1);  // a stage past the end re-reads the last k-step (never used)
@@ -269,65 +295,89 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
       }
     }
   };
-  // Chunk c8 (8 codes) of the thread's slice -> 8 bf16/f16 values in LDS.
-  auto dq_chunk = [&](const Stage& S, const Scales& Q, int c8, uint16_t* Bb) {
-    constexpr int GC = GS / 8;  // chunks per group
-    const int t = NGT > 1 ? c8 / GC : 0;
-    const float s = Q.s[t], gm = Q.g[t];
-    float cv[8];
-    if constexpr (SB == 8) {
+  // The dequant of a stage runs in NPART parts (part p covers chunks
+  // [p * C8 / NPART, (p + 1) * C8 / NPART)). With a codebook, lookup() reads a part's
+  // code values from LDS as f16 pairs one sub-step before finish() scales,
+  // converts and writes them, so the reads are in flight under MFMAs.
+  // Uniform codes are converted inside finish().
+  constexpr int NPART = NW > 4 ? 4 : 3;                  // dequant parts per stage
+  constexpr int MAXP = CB ? (C8 + NPART - 1) / NPART : 1;  // chunks in the largest part
+  struct Codes {
+    ts_f16x2 v[MAXP][4];
+  };
+  const _Float16* cbh = reinterpret_cast<const _Float16*>(cbs) + 2 * cb_lane;
+  auto cbval = [&](uint32_t c) { return cbh[c * (2 * CBC)]; };
+  auto lookup = [&](const Stage& S, int p, Codes& C) {
+    if constexpr (CB) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t d = S.w[2 * c8 + h];
+      for (int c8 = 0; c8 < C8; ++c8) {
+        if (!(c8 >= p * C8 / NPART && c8 < (p + 1) * C8 / NPART)) continue;
+        ts_f16x2* cv = C.v[c8 - p * C8 / NPART];
+        uint32_t c[8];
+        if constexpr (SB == 8) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) c[e] = (S.w[2 * c8 + (e >> 2)] >> (8 * (e & 3))) & 0xffu;
+        } else if constexpr (SB == 4) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) c[e] = (S.w[c8] >> (4 * e)) & 15u;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) c[e] = (S.w[c8 >> 1] >> (16 * (c8 & 1) + 2 * e)) & 3u;
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t c = (d >> (8 * e)) & 0xffu;
-          cv[4 * h + e] = CB ? cbs[c * CBC + cb_lane] : (float)c;
+          cv[e].x = cbval(c[2 * e]);
+          cv[e].y = cbval(c[2 * e + 1]);
         }
       }
-    } else if constexpr (SB == 4) {
-      const uint32_t d = S.w[c8];
-      if constexpr (CB) {
+    }
+  };
+  auto finish = [&](const Stage& S, const Scales& Q, int p, const Codes& C, int buf) {
+    uint16_t* Bb = Bs + buf * BN * BK;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) cv[e] = cbs[((d >> (4 * e)) & 15u) * CBC + cb_lane];
-      } else {
-        uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+    for (int c8 = 0; c8 < C8; ++c8) {
+      if (!(c8 >= p * C8 / NPART && c8 < (p + 1) * C8 / NPART)) continue;
+      constexpr int GC = GS / 8;  // chunks per group
+      const int t = NGT > 1 ? c8 / GC : 0;
+      const float sc = Q.s[t], gm = Q.g[t];
+      float cv[8];
+      if constexpr (CB) {
+        const ts_f16x2* h = C.v[c8 - p * C8 / NPART];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          cv[2 * e] = (float)h[e].x;
+          cv[2 * e + 1] = (float)h[e].y;
+        }
+      } else if constexpr (SB == 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cv[e] = (float)((S.w[2 * c8 + (e >> 2)] >> (8 * (e & 3))) & 0xffu);
+      } else if constexpr (SB == 4) {
+        uint32_t lo = S.w[c8] & 0x0f0f0f0fu, hi = (S.w[c8] >> 4) & 0x0f0f0f0fu;
         asm volatile("" : "+v"(lo), "+v"(hi));  // keeps the byte-select conversions (v_cvt_f32_ubyteN)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           cv[2 * e] = (float)((lo >> (8 * e)) & 0xffu);
           cv[2 * e + 1] = (float)((hi >> (8 * e)) & 0xffu);
         }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cv[e] = (float)((S.w[c8 >> 1] >> (16 * (c8 & 1) + 2 * e)) & 3u);
       }
-    } else {  // 2-bit: 8 codes in 16 bits
-      const uint32_t d = S.w[c8 >> 1] >> (16 * (c8 & 1));
+      float v[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t c = (d >> (2 * e)) & 3u;
-        cv[e] = CB ? cbs[c * CBC + cb_lane] : (float)c;
+      for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(cv[e], sc, gm);
+      if constexpr (RVQ) {
+        const uint32_t d2 = S.w2[c8 >> 1] >> (16 * (c8 & 1));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] += __builtin_fmaf((float)((d2 >> (2 * e)) & 3u), Q.s2[t], Q.g2[t]);
       }
+      ts_u32x4 pk;
+      pk.x = to_pair<BF16>(v[0], v[1]);
+      pk.y = to_pair<BF16>(v[2], v[3]);
+      pk.z = to_pair<BF16>(v[4], v[5]);
+      pk.w = to_pair<BF16>(v[6], v[7]);
+      *reinterpret_cast<ts_u32x4*>(Bb + swz(wr, wpart * C8 + c8)) = pk;
     }
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(cv[e], s, gm);
-    if constexpr (RVQ) {
-      const uint32_t d2 = S.w2[c8 >> 1] >> (16 * (c8 & 1));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] += __builtin_fmaf((float)((d2 >> (2 * e)) & 3u), Q.s2[t], Q.g2[t]);
-    }
-    ts_u32x4 pk;
-    pk.x = to_pair<BF16>(v[0], v[1]);
-    pk.y = to_pair<BF16>(v[2], v[3]);
-    pk.z = to_pair<BF16>(v[4], v[5]);
-    pk.w = to_pair<BF16>(v[6], v[7]);
-    *reinterpret_cast<ts_u32x4*>(Bb + swz(wr, wpart * C8 + c8)) = pk;
-  };
-  // part p of 3 covers chunks [p * C8 / 3, (p + 1) * C8 / 3)
-  auto dq_part = [&](const Stage& S, const Scales& Q, int p, int buf) {
-    uint16_t* Bb = Bs + buf * BN * BK;
-#pragma unroll
-    for (int c8 = 0; c8 < C8; ++c8)
-      if (c8 >= p * C8 / 3 && c8 < (p + 1) * C8 / 3) dq_chunk(S, Q, c8, Bb);
   };
 
   // ---- outliers: this row's entries in column order, folded into the tile --
@@ -360,16 +410,17 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
                                                 __builtin_bit_cast(ts_f16x2, dv));
         }
       }
-      if (en_stale) en = ptr < oend ? oload(ptr) : PF_NO_COL;  // second entry in one k-step
+      if (en_stale) {  // second entry in one k-step
+        const uint32_t v = ts_load_sync(a.ocs + min(ptr, oend - 1));
+        en = ptr < oend ? v : PF_NO_COL;
+      }
       e = en;
       ++ptr;
       en_stale = true;
     }
   };
-  auto fetch_outlier = [&]() {
-    if (!a.has_out) return;
-    tld = oload(min(ptr, oend > 0 ? oend - 1 : 0u));
-  };
+  // unconditional (also without outliers: roc is then a valid 4-byte dummy)
+  auto fetch_outlier = [&]() { tld = oload(min(ptr, oend > 0 ? oend - 1 : 0u)); };
 
   // ---- prologue --------------------------------------------------------------
   Stage S0, S1;
@@ -377,7 +428,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
   load_stage(0, S0);
   load_stage(1, S1);
   if constexpr (CB) {
-    for (int i = tid; i < CBN * CBC; i += NT) cbs[i] = a.codebook[i / CBC];
+    for (int i = tid; i < CBN * CBC; i += NT) cbs[i] = ts_f2h(a.codebook[i / CBC]);
   }
   if (a.has_out) {
     const int64_t r = min(n0 + wr, a.N);  // a row past N has an empty range
@@ -392,7 +443,11 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
     Scales Q;
     scales(S0, Q);
 #pragma unroll
-    for (int p = 0; p < 3; ++p) dq_part(S0, Q, p, 0);
+    for (int p = 0; p < NPART; ++p) {
+      Codes C;
+      lookup(S0, p, C);
+      finish(S0, Q, p, C, 0);
+    }
   }
   fold_outliers(0, 0);
   fetch_outlier();
@@ -419,7 +474,7 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
       F.a[i] = *reinterpret_cast<const ts_u32x4*>(Ab + swz(wm * (BM / 2) + 32 * i + (lane & 31), c));
 #pragma unroll
     for (int j = 0; j < TN; ++j)
-      F.b[j] = *reinterpret_cast<const ts_u32x4*>(Bb + swz(wn * (BN / 2) + 32 * j + (lane & 31), c));
+      F.b[j] = *reinterpret_cast<const ts_u32x4*>(Bb + swz(wn * (BN / WN) + 32 * j + (lane & 31), c));
   };
   auto mfma = [&](const Frag& F) {
 #pragma unroll
@@ -428,51 +483,111 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
       for (int j = 0; j < TN; ++j) acc[i][j] = ts_mfma32x32x16<BF16>(F.a[i], F.b[j], acc[i][j]);
   };
 
+  // Interleave a sub-step's 16 (TM * TN) MFMAs with the LDS reads, VALU work
+  // and LDS writes around them, so the matrix core is fed while the rest
+  // issues (one wave per SIMD: a wave stalled on a wait leaves it idle).
+  auto interleave = [&]() {
+    if constexpr (NW > 4) return;  // two waves per SIMD: the hardware interleaves them
+#pragma unroll
+    for (int i = 0; i < TM * TN; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+    }
+  };
+  if constexpr (NW > 4) {
+    // Two waves per SIMD: each sub-step reads its fragments just before its
+    // MFMAs and the dequant parts follow without look-ahead (the other wave
+    // on the SIMD covers the waits); one barrier at the end of the k-step.
+    // (An explicit ping-pong, the two waves of a SIMD alternating between
+    // memory and MFMA phases separated by barriers, measured slower.)
+    load_x(1, X);
+    auto kstep8 = [&](int kt, Stage& S) {
+      const int cur = kt & 1, nxt = cur ^ 1;
+      // x of kt + 1 (loaded a k-step ago) goes to nxt first, which no wave
+      // reads until after this k-step's barrier; X then takes kt + 2.
+      store_x(nxt, X);
+      load_x(kt + 2, X);
+      Scales Q;
+      scales(S, Q);
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        Frag F;
+        Codes C;
+        lookup(S, sub, C);
+        read_frag(cur, sub, F);
+        mfma(F);
+        finish(S, Q, sub, C, nxt);
+      }
+      fold_outliers(kt + 1, nxt);
+      fetch_outlier();
+      load_stage(kt + 3, S);
+      ts_lds_barrier();
+    };
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
+      kstep8(kt, S1);
+      kstep8(kt + 1, S0);
+    }
+    if (kt < KT) kstep8(kt, S1);
+  } else {
   Frag F0, F1;
+  Codes CA, CB2;
   read_frag(0, 0, F0);
-  // One k-step: x for k-step kt + 1 is loaded into X; stage S (k-step kt + 1)
-  // is dequantized into buffer nxt over sub-steps 0-2 and refilled with
+  lookup(S1, 0, CA);
+  // One k-step (S = stage kt + 1, Sn = stage kt + 2). x for k-step kt + 1 is
+  // loaded into X; S is dequantized into buffer nxt over sub-steps 0-2 (part
+  // 0's codes were looked up in the previous k-step) and refilled with
   // k-step kt + 3; X is stored to nxt; barrier; sub-step 3 runs on fragments
-  // already in registers while the next k-step's first fragments are read.
-  auto kstep = [&](int kt, Stage& S) {
+  // already in registers while the next k-step's first fragments and part 0
+  // of Sn's codes are read.
+  auto kstep = [&](int kt, Stage& S, const Stage& Sn) {
     const int cur = kt & 1, nxt = cur ^ 1;
     Scales Q;
     load_x(kt + 1, X);
     scales(S, Q);
     read_frag(cur, 1, F1);
-    __builtin_amdgcn_sched_barrier(0);
+    lookup(S, 1, CB2);
     mfma(F0);
-    dq_part(S, Q, 0, nxt);
+    finish(S, Q, 0, CA, nxt);
+    interleave();
     __builtin_amdgcn_sched_barrier(0);
     read_frag(cur, 2, F0);
-    __builtin_amdgcn_sched_barrier(0);
+    lookup(S, 2, CA);
     mfma(F1);
-    dq_part(S, Q, 1, nxt);
+    finish(S, Q, 1, CB2, nxt);
+    interleave();
     __builtin_amdgcn_sched_barrier(0);
     read_frag(cur, 3, F1);
-    __builtin_amdgcn_sched_barrier(0);
     mfma(F0);
-    dq_part(S, Q, 2, nxt);
+    finish(S, Q, 2, CA, nxt);
+    store_x(nxt, X);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
     fold_outliers(kt + 1, nxt);
     fetch_outlier();
     load_stage(kt + 3, S);
-    store_x(nxt, X);
     ts_lds_barrier();
     read_frag(nxt, 0, F0);
+    lookup(Sn, 0, CA);
     mfma(F1);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
   };
   // two k-steps per iteration (the stages alternate), one exit
   int kt = 0;
   for (; kt + 1 < KT; kt += 2) {
-    kstep(kt, S1);
-    kstep(kt + 1, S0);
+    kstep(kt, S1, S0);
+    kstep(kt + 1, S0, S1);
   }
-  if (kt < KT) kstep(kt, S1);
+  if (kt < KT) kstep(kt, S1, S0);
+  }
 
   // epilogue: bias, cast, store
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int64_t n = n0 + wn * (BN / 2) + 32 * j + (lane & 31);
+    const int64_t n = n0 + wn * (BN / WN) + 32 * j + (lane & 31);
     if (n >= a.N) continue;
     const float b = a.bias ? XT<BF16>::to_f(a.bias[n]) : 0.f;
 #pragma unroll
@@ -490,13 +605,6 @@ __global__ __launch_bounds__(256, 1) void prefill_kernel(const PrefillArgs a_in)
   }
 }
 
-template <int BITS, bool CB, int BN>
-constexpr size_t prefill_smem() {
-  constexpr int CBN = CB ? (1 << BITS) : 0;
-  constexpr int CBC = (CB && BITS == 8) ? 16 : 32;
-  return (size_t)2 * (PF_BM + BN) * PF_BK * 2 + (size_t)CBN * CBC * 4;
-}
-
 // Raises a kernel's dynamic LDS limit once per device (thread safe).
 inline bool ts_set_smem_once(const void* kern, size_t smem, std::once_flag* flags, bool* ok) {
   int dev = 0;
@@ -507,17 +615,23 @@ inline bool ts_set_smem_once(const void* kern, size_t smem, std::once_flag* flag
   return ok[dev];
 }
 
-template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN>
+template <int BITS, bool CB, int BN>
+constexpr size_t prefill_smem() {
+  constexpr int CBN = CB ? (1 << BITS) : 0;
+  return (size_t)2 * (PF_BM + BN) * PF_BK * 2 + (size_t)CBN * 32 * 4;
+}
+
+template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN, int NW>
 inline int launch_prefill(PrefillArgs a, hipStream_t st) {
   constexpr size_t smem = prefill_smem<BITS, CB, BN>();
-  static_assert(smem <= 160 * 1024, "LDS budget");
-  auto kern = prefill_kernel<BITS, GS, BF16, CB, RVQ, DQ, BN>;
+  static_assert(smem <= 160 * 1024, "LDS budget (160 KB per CU)");
+  auto kern = prefill_kernel<BITS, GS, BF16, CB, RVQ, DQ, BN, NW>;
   static std::once_flag flags[64];
   static bool ok[64];
   if (!ts_set_smem_once(reinterpret_cast<const void*>(kern), smem, flags, ok)) return TS_HIP_ERROR;
   a.m_tiles = ts_cdiv(a.M, PF_BM);
   a.n_tiles = ts_cdiv(a.N, BN);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(a.m_tiles * a.n_tiles)), dim3(256), smem, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(a.m_tiles * a.n_tiles)), dim3(64 * NW), smem, st, a);
   TS_CHECK_LAUNCH();
   return TS_OK;
 }
@@ -525,14 +639,14 @@ inline int launch_prefill(PrefillArgs a, hipStream_t st) {
 // 256 x 256 tiles when they fill the CUs, else 256 x 128.
 template <int BITS, int GS, bool BF16, bool CB, bool RVQ>
 inline int launch_prefill_tiles(PrefillArgs& a, hipStream_t st) {
-  const bool wide = ts_cdiv(a.M, PF_BM) * ts_cdiv(a.N, 256) >= 256;
   const bool dq = a.dqsc != nullptr;
+  const bool wide = ts_cdiv(a.M, PF_BM) * ts_cdiv(a.N, 256) >= 256;
   if (wide) {
-    return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 256>(a, st)
-              : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 256>(a, st);
+    return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 256, PF_NW_WIDE>(a, st)
+              : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 256, PF_NW_WIDE>(a, st);
   }
-  return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128>(a, st)
-            : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128>(a, st);
+  return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, 4>(a, st)
+            : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128, 4>(a, st);
 }
 
 // Per-(bit width, group size) launchers, one translation unit each
