@@ -168,6 +168,20 @@ int ts_tile_outlier_max(const int32_t* outlier_row_ptr, int64_t rows, int32_t* m
 int ts_build_tile_outliers(const int32_t* outlier_row_ptr, const int32_t* outlier_row, const int32_t* outlier_col,
                            const uint16_t* outlier_delta, int64_t rows, int64_t cap, uint64_t* slots, void* stream);
 
+/*
+ * ts_build_outlier_tables with no workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc). No counterpart in the reference. The sort scratch is a
+ * fixed 8 MiB device array inside the library (one per GPU, held until the
+ * process ends): the call allocates nothing, and n_outliers is limited to
+ * 262144 (TS_BAD_ARG above; the config-scale layers hold at most 234,881).
+ * All calls on one GPU share that array, so calls that overlap on one GPU
+ * (concurrent streams or host threads) race; order them on one stream.
+ */
+int ts_build_outlier_tables_noalloc(const ts_qlayer* layer, const int32_t* outlier_idx, const uint16_t* outlier_val,
+                                    int64_t n_outliers, int32_t* outlier_row, int32_t* outlier_col,
+                                    uint16_t* outlier_delta, int32_t* outlier_row_ptr, void* stream);
+
 /* ts_qlayer.outlier_colsorted from the row-sorted CSR tables: each row's
  * entries (col | f16 delta << 16) sorted by column. out: u32 [n_outliers].
  * Needs every column below 65535. */

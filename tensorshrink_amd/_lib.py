@@ -73,6 +73,8 @@ PROTOTYPES = {
     "ts_tile_outlier_max": (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp]),
     "ts_build_tile_outliers": (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp]),
     "ts_build_colsorted_outliers": (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
+    "ts_build_outlier_tables_noalloc": (ctypes.c_int, [ctypes.POINTER(QLayer), c_vp, c_vp, c_i64, c_vp, c_vp, c_vp,
+                                                       c_vp, c_vp]),
     "ts_build_outlier_tables": (ctypes.c_int, [ctypes.POINTER(QLayer), c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp,
                                                c_vp, c_sz, c_vp]),
     "ts_topk_workspace_bytes": (c_sz, [c_i64, c_i64]),

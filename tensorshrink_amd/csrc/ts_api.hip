@@ -37,6 +37,8 @@ int build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t*
 int apply_outlier_correction(float* out, int64_t M, int64_t ldo, const void* x, int64_t ldx, int xdt,
                              const int32_t* row_ptr, const int32_t* col, const uint16_t* delta, int64_t rows,
                              hipStream_t st);
+int build_outlier_tables_noalloc(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n,
+                                 int32_t* orow, int32_t* ocol, uint16_t* odelta, int32_t* row_ptr, hipStream_t st);
 size_t topk_ws_bytes(int64_t n, int64_t k);
 int topk_count(const ts_qinput* in, int64_t k, void* ws, size_t ws_bytes, int64_t* n_cand, hipStream_t st);
 int topk_write(const ts_qinput* in, int64_t k, void* ws, int64_t* cidx, float* cval, hipStream_t st);
@@ -184,6 +186,13 @@ int ts_build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16
   if (!L || !L->packed || n < 0 || (n > 0 && (!idx || !val || !orow || !ocol || !odelta))) return TS_BAD_ARG;
   if (n > 0 && (L->rows * L->cols) > ((int64_t)1 << 31)) return TS_NOT_COVERED;  // int32 flat indices
   return ts::build_outlier_tables(L, idx, val, n, orow, ocol, odelta, row_ptr, ws, ws_bytes, S(stream));
+}
+
+int ts_build_outlier_tables_noalloc(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n,
+                                    int32_t* orow, int32_t* ocol, uint16_t* odelta, int32_t* row_ptr, void* stream) {
+  if (!L || !L->packed || n < 0 || (n > 0 && (!idx || !val || !orow || !ocol || !odelta))) return TS_BAD_ARG;
+  if (n > 0 && (L->rows * L->cols) > ((int64_t)1 << 31)) return TS_NOT_COVERED;  // int32 flat indices
+  return ts::build_outlier_tables_noalloc(L, idx, val, n, orow, ocol, odelta, row_ptr, S(stream));
 }
 
 size_t ts_topk_workspace_bytes(int64_t n, int64_t k) { return (k > 0 && k < n) ? ts::topk_ws_bytes(n, k) : 0; }

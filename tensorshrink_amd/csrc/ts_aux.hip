@@ -7,6 +7,8 @@
 
 #include <rocprim/rocprim.hpp>
 
+#include <mutex>
+
 #include "ts_common.h"
 
 namespace ts {
@@ -406,6 +408,51 @@ int build_outlier_tables(const ts_qlayer* L, const int32_t* idx, const uint16_t*
   TS_CHECK_LAUNCH();
   if (row_ptr) return outlier_row_ptr(orow, n, L->rows, row_ptr, st);
   return TS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// ts_build_outlier_tables without a caller workspace: the sort scratch is a
+// fixed device array, so the call allocates nothing (for callers that cannot
+// call hipMalloc: graph capture, serving loops). Host code reaches the array
+// only through the address hipGetSymbolAddress returns for the current
+// device (each device holds its own copy); the array's name is a host-side
+// stand-in that is never passed to a kernel or copy. Every call on one device
+// shares the array, so calls that overlap on one device race; the sort writes
+// every scratch byte it reads, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(8) << 20;
+constexpr int64_t NOALLOC_MAX_OUTLIERS = 262144;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+void* g_scratch[MAX_DEVICES];
+int g_scratch_rc[MAX_DEVICES];
+std::once_flag g_scratch_once[MAX_DEVICES];
+
+// Device address of `scratch` on the current device, looked up once per device.
+int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return TS_HIP_ERROR;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess && p ? TS_OK : TS_HIP_ERROR;
+    g_scratch[dev] = p;
+  });
+  *out = g_scratch[dev];
+  return g_scratch_rc[dev];
+}
+}  // namespace
+
+int build_outlier_tables_noalloc(const ts_qlayer* L, const int32_t* idx, const uint16_t* val, int64_t n,
+                                 int32_t* orow, int32_t* ocol, uint16_t* odelta, int32_t* row_ptr, hipStream_t st) {
+  if (n > NOALLOC_MAX_OUTLIERS) return TS_BAD_ARG;
+  const size_t need = n > 0 ? outlier_tables_ws(n) : 0;
+  if (need > NOALLOC_SCRATCH_BYTES) return TS_WORKSPACE;
+  void* p = nullptr;
+  const int rc = scratch_address(&p);
+  if (rc != TS_OK) return rc;
+  return build_outlier_tables(L, idx, val, n, orow, ocol, odelta, row_ptr, p, NOALLOC_SCRATCH_BYTES, st);
 }
 
 // Largest outlier count over 16-row tiles: one workgroup, strided over tiles.
