@@ -524,14 +524,28 @@ struct GroupArgs {
   float* gmin32;
 };
 
+// NaN-propagating min / max, as torch's amin/amax and numpy's min/max
+// (codec.py:566-567, 395-396); equal to fminf / fmaxf when neither is NaN.
+TS_DEV float nan_min(float a, float b) { return a != a ? a : (b != b ? b : fminf(a, b)); }
+TS_DEV float nan_max(float a, float b) { return a != a ? a : (b != b ? b : fmaxf(a, b)); }
+// max(x, lo) keeping NaN, as torch's clamp(min=) and numpy's maximum do.
+TS_DEV float nan_floor(float x, float lo) { return x != x ? x : fmaxf(x, lo); }
+
 TS_DEV float load_clamped(const GroupArgs& a, int64_t r, int64_t c) {
   const int64_t src = c < a.cols ? c : a.cols - 1;  // pad with the last column (codec.py:555-560)
   float v = load_w(a.w, a.dt, r * a.cols + src);
-  if (a.clamp) v = fminf(fmaxf(v, -a.t), a.t);
+  // flat.clamp_(-t, t) (codec.py:543): NaN stays NaN, and a NaN bound (t is
+  // the top-k minimum, NaN once a NaN weight is among the top k) makes every
+  // element NaN.
+  if (a.clamp) v = a.t != a.t ? a.t : (v != v ? v : fminf(fmaxf(v, -a.t), a.t));
   return v;
 }
 
 TS_DEV uint32_t assign_code(float v, int levels, const float* mids, int n_mids) {
+  // NaN: torch.searchsorted sorts it after every mid (the last code after
+  // the clamp, codec.py:371-372); the uniform grid's round/clamp/uint8 cast
+  // gives 0 on the reference's CPU.
+  if (v != v) return mids ? (uint32_t)n_mids : 0u;
   if (!mids) {
     float c = rintf(v);
     c = fminf(fmaxf(c, 0.f), (float)levels);
@@ -564,15 +578,15 @@ __global__ __launch_bounds__(256) void quant_groups_kernel(const GroupArgs a) {
   for (int e = 0; e < 8; ++e) v[e] = load_clamped(a, r, live ? c0 + e : a.cols - 1);
   float mn = v[0], mx = v[0];
 #pragma unroll
-  for (int e = 1; e < 8; ++e) { mn = fminf(mn, v[e]); mx = fmaxf(mx, v[e]); }
+  for (int e = 1; e < 8; ++e) { mn = nan_min(mn, v[e]); mx = nan_max(mx, v[e]); }
 #pragma unroll
   for (int o = 1; o < GL; o <<= 1) {
-    mn = fminf(mn, __shfl_xor(mn, o, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mn = nan_min(mn, __shfl_xor(mn, o, 64));
+    mx = nan_max(mx, __shfl_xor(mx, o, 64));
   }
   const int levels = (1 << a.bits) - 1;
   float scale = (mx - mn) / (float)levels;
-  scale = fmaxf(scale, 1e-8f);
+  scale = nan_floor(scale, 1e-8f);
   if (!live) return;
   uint32_t code[8];
 #pragma unroll
@@ -624,10 +638,10 @@ __global__ void quant_groups_generic_kernel(const GroupArgs a) {
   const int64_t r = id / a.n_groups, g = id % a.n_groups;
   const int64_t c0 = g * a.gs;
   float mn = load_clamped(a, r, c0), mx = mn;
-  for (int e = 1; e < a.gs; ++e) { const float v = load_clamped(a, r, c0 + e); mn = fminf(mn, v); mx = fmaxf(mx, v); }
+  for (int e = 1; e < a.gs; ++e) { const float v = load_clamped(a, r, c0 + e); mn = nan_min(mn, v); mx = nan_max(mx, v); }
   const int levels = (1 << a.bits) - 1;
   float scale = (mx - mn) / (float)levels;
-  scale = fmaxf(scale, 1e-8f);
+  scale = nan_floor(scale, 1e-8f);
   uint8_t* prow = a.packed + r * a.pstride;
   const int per = 8 / a.bits;  // codes per byte
   uint32_t last = 0;
@@ -778,23 +792,23 @@ __global__ __launch_bounds__(256) void dq_kernel(const uint16_t* vals, int64_t n
   for (int i = threadIdx.x; i < dqgs; i += blockDim.x) {
     const int64_t f = base + i;
     const float v = ts_h2f(vals[f < n ? f : n - 1]);
-    mn = fminf(mn, v);
-    mx = fmaxf(mx, v);
+    mn = nan_min(mn, v);
+    mx = nan_max(mx, v);
   }
   smn[threadIdx.x] = mn;
   smx[threadIdx.x] = mx;
   __syncthreads();
   for (int s = 128; s > 0; s >>= 1) {
     if ((int)threadIdx.x < s) {
-      smn[threadIdx.x] = fminf(smn[threadIdx.x], smn[threadIdx.x + s]);
-      smx[threadIdx.x] = fmaxf(smx[threadIdx.x], smx[threadIdx.x + s]);
+      smn[threadIdx.x] = nan_min(smn[threadIdx.x], smn[threadIdx.x + s]);
+      smx[threadIdx.x] = nan_max(smx[threadIdx.x], smx[threadIdx.x + s]);
     }
     __syncthreads();
   }
   mn = smn[0];
   mx = smx[0];
   float ms = (mx - mn) / 255.0f;
-  ms = fmaxf(ms, 1e-8f);
+  ms = nan_floor(ms, 1e-8f);
   const uint16_t ms16 = ts_f2h(ms), mn16 = ts_f2h(mn);
   if (threadIdx.x == 0) { meta[2 * blockIdx.x] = ms16; meta[2 * blockIdx.x + 1] = mn16; }
   const float msr = ts_h2f(ms16), mnr = ts_h2f(mn16);

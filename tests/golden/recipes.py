@@ -70,3 +70,47 @@ LLAMA3_70B_LINEARS = (
 def layer_seed(index: int) -> int:
     """Seed for linear number `index` (q, k, v, o, gate, up, down = 0..6)."""
     return 1000 + index
+
+
+def tiny_model(seed: int = 11):
+    """A small decoder-shaped module tree for the module-level API tests:
+    eligible linears (q/up/down in two blocks, mixed weight distributions so
+    that the adaptive chain lands on different bit widths) next to ones the
+    default skip rules exclude by name (norm, embed, lm_head) or size
+    (numel < 16384). fp16 weights from the torch CPU generator."""
+    import torch.nn as nn
+
+    d, f = 256, 512
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj = nn.Linear(d, d, bias=False)
+            self.up_proj = nn.Linear(d, f, bias=True)
+            self.down_proj = nn.Linear(f, d, bias=False)
+            self.input_norm = nn.Linear(d, d, bias=False)
+
+    class Tiny(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.embed_tokens = nn.Linear(d, d, bias=False)
+            self.layers = nn.ModuleList([Block(), Block()])
+            self.lm_head = nn.Linear(d, 64, bias=False)
+            self.tiny = nn.Linear(32, 32)
+
+    m = Tiny()
+    g = torch.Generator().manual_seed(seed)
+    for i, (name, mod) in enumerate(sorted(m.named_modules(), key=lambda t: t[0])):
+        if not isinstance(mod, nn.Linear):
+            continue
+        n, k = mod.weight.shape
+        if "up_proj" in name:  # heavy tails: 4-bit error above typical thresholds
+            w = student_t_weight(n, k, seed * 100 + i)
+        elif "q_proj" in name and name.startswith("layers.1"):  # few distinct levels: 2-bit suffices
+            w = tie_heavy_weight(n, k, seed * 100 + i, levels=2)
+        else:
+            w = gaussian_weight(n, k, seed * 100 + i)
+        mod.weight.data = w.to(torch.float16)
+        if mod.bias is not None:
+            mod.bias.data = (torch.randn(n, generator=g) * 0.05).to(torch.float16)
+    return m

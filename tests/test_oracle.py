@@ -1,6 +1,7 @@
 """The CPU oracle against the reference's golden vectors, library routines and
 closed-form properties. CPU only."""
 import hashlib
+import os
 
 import numpy as np
 import pytest
@@ -160,3 +161,28 @@ def test_oracle_config_digests(name):
             continue
         assert hashlib.sha256(np.ascontiguousarray(q[f]).tobytes()).hexdigest() == h, f
     assert hashlib.sha256(O.dequantize(q, "f32").tobytes()).hexdigest() == dig["digests"]["deq_f32"]
+
+
+def test_oracle_nan_weights_match_reference():
+    """NaN weights (api_fixtures.json, written from the reference): the oracle
+    propagates NaN through the clamp, the group min/max, the scale floor and
+    the double quantization exactly as the reference's torch/numpy code."""
+    import json
+    import warnings
+    fix = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                      "api_fixtures.json")))["nan_weights"]
+    for case, ref in fix.items():
+        w = recipes.gaussian_weight(16, 256, 44)
+        w.view(-1)[[3, 1000, 2047]] = float("nan")
+        kw = ref["kw"]
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore", RuntimeWarning)  # NaN -> uint8 casts, as in the reference
+            q = O.quantize(w, bits=kw["bits"], group_size=64, outlier_frac=kw.get("outlier_frac", 0.001),
+                           double_quant=kw.get("double_quant", False), nf_quant=kw.get("nf_quant", False))
+        for f, exp in ref.items():
+            if f == "kw":
+                continue
+            v = np.ascontiguousarray(q[f])
+            bits = v.view(np.uint16) if v.dtype == np.float16 else v
+            np.testing.assert_array_equal(bits.reshape(-1), np.asarray(exp["values"], dtype=bits.dtype),
+                                          err_msg=f"{case}: {f}")
