@@ -18,6 +18,8 @@ from .codec import (
 from .config import TensorShrinkConfig
 from .gpu_quantize import quantize_module_gpu, quantize_tensor_gpu, quantize_tensor_gpu_adaptive
 from .kernels import apply_outlier_correction, dequantize_weight, fused_quantized_linear
-from .modules import DEFAULT_SKIP_PATTERNS, T5_EXTRA_SKIP_PATTERNS, QuantLinear, quantize_module
+from .container import ContainerReader, ContainerWriter, save_container, stream_quantize_safetensors_dir
+from .modules import (DEFAULT_SKIP_PATTERNS, T5_EXTRA_SKIP_PATTERNS, QuantLinear, load_quantized_module,
+                      quantize_module, save_quant_module)
 
 __version__ = "0.4.0+mi355x"

@@ -511,3 +511,75 @@ def quantize_module(
         record(name, qlin, err, esc, f32, lin.weight.element_size())
     stats["ratio"] = stats["orig_bytes"] / max(1, stats["packed_bytes"]) if stats["orig_bytes"] > 0 else 1.0
     return stats
+
+
+# ---------------------------------------------------------------------------
+# container save / load (modules.py:1458-1562)
+# ---------------------------------------------------------------------------
+
+def save_quant_module(model: nn.Module, path, verbose: bool = True) -> dict:
+    """Write a quantized model to a .tsk container (modules.py:1458-1496):
+    each QuantLinear's weight as a quantized entry straight from its packed
+    buffers (scale/gmin as f16, outlier values as f16(base + delta), as
+    QuantLinear.to_quantized_tensor rebuilds them), its bias raw, and every
+    other state_dict entry raw; a QuantLinear's own buffers are not repeated."""
+    from .container import ContainerWriter
+    written, prefixes = set(), []
+    with ContainerWriter(path) as w:
+        for name, mod in model.named_modules():
+            if not isinstance(mod, QuantLinear):
+                continue
+            w.add_quantized(f"{name}.weight", mod.to_quantized_tensor(), force_fp32_compute=mod.force_fp32_compute)
+            written.add(f"{name}.weight")
+            prefixes.append(f"{name}.")
+            if mod.bias is not None:
+                w.add_raw(f"{name}.bias", mod.bias)
+                written.add(f"{name}.bias")
+        n_raw = 0
+        for key, t in model.state_dict().items():
+            if key in written or any(key.startswith(p) for p in prefixes):
+                continue
+            w.add_raw(key, t)
+            n_raw += 1
+    if verbose:
+        print(f"  saved {len(written)} quantized tensors + {n_raw} raw tensors -> {path}")
+    return {"n_quant": len(written), "n_raw": n_raw}
+
+
+def load_quantized_module(model: nn.Module, reader, max_dequant_rows: Union[int, str] = DEFAULT_MAX_DEQUANT_ROWS,
+                          cache_budget_mb: float = 0.0, host_cache_budget_mb: float = 0.0,
+                          fast_dequant: bool = True, use_triton: bool = True, parallel: bool = True,
+                          verbose: bool = True) -> dict:
+    """Populate a freshly built model from a container (modules.py:1499-1562):
+    every nn.Linear whose "<name>.weight" is a quantized entry becomes a
+    QuantLinear built from the packed data on the current GPU (frames
+    decompressed in parallel threads with `parallel`), with the entry's
+    force_fp32_compute flag; the raw entries the model's state_dict names are
+    loaded with load_state_dict(strict=False)."""
+    if cache_budget_mb > 0 or host_cache_budget_mb > 0:
+        raise NotImplementedError("WeightCache is not part of the tensorshrink_amd path")
+    names = set(reader.names())
+    targets = []
+    for name, mod in list(model.named_modules()):
+        if isinstance(mod, nn.Linear) and not isinstance(mod, QuantLinear):
+            wkey, bkey = f"{name}.weight", f"{name}.bias"
+            if wkey in names and reader.kind(wkey) == "quant":
+                f32 = bool(reader.manifest["tensors"][wkey].get("force_fp32_compute", False))
+                targets.append((name, wkey, bkey if bkey in names else None, f32))
+    keys = [t[1] for t in targets]
+    qts = reader.get_quantized_many(keys) if parallel and len(keys) > 1 else {k: reader.get_quantized(k)
+                                                                              for k in keys}
+    for name, wkey, bkey, f32 in targets:
+        bias = reader.get(bkey) if bkey is not None else None
+        q = QuantLinear.from_quantized_tensor(qts[wkey], bias, max_dequant_rows=max_dequant_rows,
+                                              force_fp32_compute=f32, fast_dequant=fast_dequant,
+                                              use_triton=use_triton)
+        _set_module_by_name(model, name, q)
+        if verbose:
+            print(f"  loaded quantized: {name}")
+    keys_now = set(model.state_dict().keys())
+    raw = {n: reader.get(n) for n in names if n in keys_now and reader.kind(n) == "raw"}
+    model.load_state_dict(raw, strict=False)
+    if verbose:
+        print(f"  loaded {len(raw)} raw tensors, replaced {len(targets)} Linear layers")
+    return {"n_quant_replaced": len(targets), "n_raw_loaded": len(raw), "cache": None}
