@@ -16,10 +16,12 @@ from .codec import (
     relative_error,
 )
 from .config import TensorShrinkConfig
-from .gpu_quantize import quantize_module_gpu, quantize_tensor_gpu, quantize_tensor_gpu_adaptive
-from .kernels import apply_outlier_correction, dequantize_weight, fused_quantized_linear
 from .container import ContainerReader, ContainerWriter, save_container, stream_quantize_safetensors_dir
+from .gpu_quantize import quantize_module_gpu, quantize_tensor_gpu, quantize_tensor_gpu_adaptive
+from .graphs import CUDAGraphQuantModel
+from .kernels import apply_outlier_correction, dequantize_weight, fused_quantized_linear
 from .modules import (DEFAULT_SKIP_PATTERNS, T5_EXTRA_SKIP_PATTERNS, QuantLinear, load_quantized_module,
                       quantize_module, save_quant_module)
+from .streaming import StreamingQuantModel, stream_offload_module
 
 __version__ = "0.4.0+mi355x"

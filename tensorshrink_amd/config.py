@@ -1,8 +1,8 @@
 """TensorShrinkConfig: the quantization_config surface of hf_integration.py:77-195.
 
-Same fields, defaults, validation and dict/JSON round trip. Only the API
-surface is kept: registration with transformers' quantizer tables (the
-HfQuantizer plugin) is not part of this path.
+Same fields, defaults, validation and dict/JSON round trip. Constructing one
+registers the quantizer plugin (tensorshrink_amd.hf_integration) with
+transformers, so it can be passed to `from_pretrained(quantization_config=...)`.
 """
 from __future__ import annotations
 
@@ -26,6 +26,8 @@ class TensorShrinkConfig:
                  fast_dequant: bool = True, use_triton: bool = True, vram_budget_mb: Optional[float] = None,
                  quantize_workers: Optional[int] = 4, verbose: bool = True, companded: bool = False,
                  double_quant: bool = True, dq_group_size: Optional[int] = None, nf_quant: bool = True, **kwargs):
+        from .hf_integration import _install
+        _install()  # registers the quantizer with transformers, once
         self.quant_method = TensorShrinkQuantizationMethod.TENSORSHRINK
         self.bits = bits
         self.group_size = group_size

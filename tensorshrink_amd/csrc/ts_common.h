@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/tensorshrink_hip.h"
 
 #define TS_DEV __device__ __forceinline__
@@ -125,3 +127,14 @@ TS_DEV void ts_lds_barrier() {
   } while (0)
 
 __host__ __device__ inline int64_t ts_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Raises a kernel's dynamic LDS limit once per device, thread safe: each
+// caller owns a flags/ok pair of 64 entries (one per device ordinal).
+inline bool ts_set_smem_once(const void* kern, size_t smem, std::once_flag* flags, bool* ok) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  std::call_once(flags[dev], [&] {
+    ok[dev] = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) == hipSuccess;
+  });
+  return ok[dev];
+}

@@ -919,13 +919,9 @@ inline int launch_decode_x(const DecodeGroup& g_in, hipStream_t st) {
   const DecodeArgs& a = g.a[0];
   const size_t smem = decode_smem<BITS, CB8, RVQ, REP, XM, W, RT>(a.M, a.K, XM != XM_GLOBAL && XM != XM_DPP);
   auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB, RT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess)
-      return TS_HIP_ERROR;
-    attr_set = true;
-  }
+  static std::once_flag flags[64];
+  static bool ok[64];
+  if (!ts_set_smem_once(reinterpret_cast<const void*>(kern), 160 * 1024, flags, ok)) return TS_HIP_ERROR;
   // one workgroup per 16-row tile; tiles beyond the resident capacity are
   // scheduled by the hardware as workgroups retire
   hipLaunchKernelGGL(kern, dim3((unsigned)g.tile_end[g.n - 1]), dim3(64 * W), smem, st, g);

@@ -605,16 +605,6 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   }
 }
 
-// Raises a kernel's dynamic LDS limit once per device (thread safe).
-inline bool ts_set_smem_once(const void* kern, size_t smem, std::once_flag* flags, bool* ok) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-  std::call_once(flags[dev], [&] {
-    ok[dev] = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) == hipSuccess;
-  });
-  return ok[dev];
-}
-
 template <int BITS, bool CB, int BN>
 constexpr size_t prefill_smem() {
   constexpr int CBN = CB ? (1 << BITS) : 0;

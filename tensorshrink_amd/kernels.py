@@ -34,13 +34,21 @@ def tile_outlier_slots(row_ptr: torch.Tensor, outlier_row: torch.Tensor, outlier
     """Per-16-row-tile outlier slots for the decode kernel (ts_build_tile_outliers):
     returns (slots u64 as int64 [n_tiles * cap], cap). cap is the largest
     per-tile count rounded up to a multiple of 8; reading it back syncs the
-    stream, so QuantLinear builds the table once at construction."""
+    stream, so QuantLinear builds the table once at construction.
+
+    Every tile is padded to the fullest tile's count, so outliers crowded
+    into a few tiles would inflate the table: past max(4 x (n + 8 x tiles),
+    2^20) slots (8 MiB) no table is built and (empty, 0) is returned; the
+    decode kernel then reports the layer as not covered and the forward takes
+    the generic kernel."""
     dev = row_ptr.device
     lib = L.lib()
     mx = torch.empty(1, dtype=torch.int32, device=dev)
     L.check(lib.ts_tile_outlier_max(row_ptr.data_ptr(), rows, mx.data_ptr(), L.stream_ptr(dev)), "tile outlier count")
     cap = max(8, (int(mx.item()) + 7) // 8 * 8)
     n_tiles = (rows + 15) // 16
+    if n_tiles * cap > max(4 * (outlier_row.numel() + 8 * n_tiles), 1 << 20):
+        return torch.zeros(0, dtype=torch.int64, device=dev), 0
     slots = torch.empty(n_tiles * cap, dtype=torch.int64, device=dev)
     L.check(lib.ts_build_tile_outliers(row_ptr.data_ptr(), outlier_row.data_ptr(), outlier_col.data_ptr(),
                                        outlier_delta.data_ptr(), rows, cap, slots.data_ptr(), L.stream_ptr(dev)),
@@ -51,7 +59,11 @@ def tile_outlier_slots(row_ptr: torch.Tensor, outlier_row: torch.Tensor, outlier
 # Derived outlier tables per set of outlier buffers, so that repeated calls
 # with the same QuantLinear-style buffers neither rebuild them nor sync the
 # host (the first call builds them; later calls, including ones under graph
-# capture, reuse them). Keyed on the buffers' storage and version.
+# capture, reuse them). Keyed on the buffers' storage and version. A first
+# call made under graph capture builds the row offsets and column-sorted
+# copy inside the graph (they are then rebuilt on every replay, and not
+# cached: their contents exist only once the graph runs) and no tile slots,
+# which need a host read; the launch then takes the MFMA or generic kernel.
 _DERIVED: dict = {}
 _DERIVED_MAX = 256
 
@@ -60,8 +72,9 @@ def _derived_outliers(outlier_row, outlier_col, outlier_delta, rows: int, need_s
     key = (outlier_row.device.index, outlier_row.data_ptr(), outlier_row.numel(), outlier_row._version,
            outlier_col.data_ptr(), outlier_col._version, outlier_delta.data_ptr(), outlier_delta._version, rows)
     ent = _DERIVED.get(key)
+    capturing = torch.cuda.is_current_stream_capturing()
     if ent is None:
-        if len(_DERIVED) >= _DERIVED_MAX:
+        if len(_DERIVED) >= _DERIVED_MAX and not capturing:
             _DERIVED.pop(next(iter(_DERIVED)))
         dev = outlier_row.device
         rp = _row_ptr(outlier_row, rows)
@@ -70,8 +83,10 @@ def _derived_outliers(outlier_row, outlier_col, outlier_delta, rows: int, need_s
                                                     rows, ocs.data_ptr(), L.stream_ptr(dev)), "column-sorted outliers")
         ent = {"rp": rp, "ocs": ocs, "slots": None, "cap": 0,
                "keep": (outlier_row, outlier_col, outlier_delta)}
+        if capturing:
+            return ent
         _DERIVED[key] = ent
-    if need_slots and ent["slots"] is None:
+    if need_slots and ent["slots"] is None and not capturing:
         ent["slots"], ent["cap"] = tile_outlier_slots(ent["rp"], outlier_row, outlier_col, outlier_delta, rows)
     return ent
 
@@ -125,7 +140,7 @@ def fused_quantized_linear(
         s.outlier_row_ptr = ent["rp"].data_ptr()
         if s.padded_cols < 65535:
             s.outlier_colsorted = ent["ocs"].data_ptr()
-        if ent["slots"] is not None:  # the decode kernel reads outliers per tile
+        if ent["slots"] is not None and ent["cap"] > 0:  # the decode kernel reads outliers per tile
             s.tile_outliers, s.tile_outlier_cap = ent["slots"].data_ptr(), ent["cap"]
     ydt = torch.float32 if return_fp32 else compute_dtype
     if out is None or out.shape != (M, out_features) or out.dtype != ydt or not out.is_contiguous():

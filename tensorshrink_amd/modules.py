@@ -9,14 +9,20 @@ the same arguments. The forward runs one libtensorshrink_hip launch per call
 correction and bias fused; there is no CPU or PyTorch fallback path.
 
 Additions over the reference:
-  * ``outlier_row_ptr`` - non-persistent int32 [rows + 1] CSR offsets into the
-    row-sorted outlier tables (derived data, absent from state_dict);
-  * ``tile_outliers`` - non-persistent per-16-row-tile outlier slots (u64:
-    col, row in tile, f16 delta; ``tile_outlier_cap`` slots per tile) that
-    the decode kernel reads at a fixed address (derived data);
-  * ``outlier_colsorted`` - non-persistent per-row column-sorted outliers
-    (u32: col | f16 delta << 16) that the prefill kernel walks while it
-    dequantizes a row (derived data);
+  * derived tensors, built from the outlier buffers at construction and kept
+    as plain attributes (not buffers: absent from state_dict, and left alone
+    by loaders that re-create non-persistent buffers), which ``_apply`` moves
+    with the module:
+    ``outlier_row_ptr`` - int32 [rows + 1] CSR offsets into the row-sorted
+    outlier tables;
+    ``tile_outliers`` - per-16-row-tile outlier slots (u64: col, row in tile,
+    f16 delta; ``tile_outlier_cap`` slots per tile) that the decode kernel
+    reads at a fixed address;
+    ``outlier_colsorted`` - per-row column-sorted outliers (u32: col | f16
+    delta << 16) that the prefill kernel walks while it dequantizes a row;
+  * the kernel view (raw addresses of every tensor the kernels read) is
+    rebuilt whenever one of those tensors is reassigned or the module is
+    moved or cast;
   * 6-bit RVQ layers register ``stage2_packed``, ``stage2_scale`` and
     ``stage2_gmin`` (the reference QuantLinear cannot serve bits=6).
 ``WeightCache`` (a dense-weight cache) is not part of this path: passing
@@ -129,7 +135,7 @@ class QuantLinear(nn.Module):
         self.register_buffer("outlier_row", orow)
         self.register_buffer("outlier_col", ocol)
         self.register_buffer("outlier_delta", odelta)
-        self.register_buffer("outlier_row_ptr", rptr, persistent=False)
+        self.outlier_row_ptr = rptr
         # derived per-tile slots for the decode kernel (fixed-address loads)
         if n > 0:
             from .kernels import tile_outlier_slots
@@ -137,7 +143,7 @@ class QuantLinear(nn.Module):
                 slots, self.tile_outlier_cap = tile_outlier_slots(rptr, orow, ocol, odelta, self.rows)
         else:
             slots, self.tile_outlier_cap = torch.zeros(0, dtype=torch.int64, device=dev), 0
-        self.register_buffer("tile_outliers", slots, persistent=False)
+        self.tile_outliers = slots
         # derived column-sorted copy per row for the prefill kernel
         ocs = torch.empty(n, dtype=torch.int32, device=dev)
         if n > 0:
@@ -145,7 +151,7 @@ class QuantLinear(nn.Module):
                 L.check(lib.ts_build_colsorted_outliers(rptr.data_ptr(), ocol.data_ptr(), odelta.data_ptr(),
                                                         self.rows, ocs.data_ptr(), L.stream_ptr(dev)),
                         "column-sorted outliers")
-        self.register_buffer("outlier_colsorted", ocs, persistent=False)
+        self.outlier_colsorted = ocs
         if bias is not None:
             self.register_buffer("bias", bias.detach().clone().to(dev))
         else:
@@ -153,6 +159,7 @@ class QuantLinear(nn.Module):
         self._layer = None
         self._bias_cache = {}
         self._rebuild_cache()
+        self._view_tracking = True
 
     # -- kernel view -----------------------------------------------------
     def _make_layer(self, with_outliers: bool = True) -> L.QLayer:
@@ -172,8 +179,12 @@ class QuantLinear(nn.Module):
             s.gmin = self.gmin.data_ptr()
         if self.companded:
             s.codebook = self.codebook.data_ptr()
-            # host copy kept alive with the view (decode takes <= 16 entries as launch arguments)
-            self._codebook_host = np.ascontiguousarray(self.codebook.detach().cpu().numpy(), dtype=np.float32)
+            # host copy kept alive with the view (decode takes <= 16 entries as
+            # launch arguments); read back only when the codebook changed
+            key = (id(self.codebook), self.codebook.data_ptr(), self.codebook._version)
+            if getattr(self, "_codebook_key", None) != key:
+                self._codebook_host = np.ascontiguousarray(self.codebook.detach().cpu().numpy(), dtype=np.float32)
+                self._codebook_key = key
             s.codebook_host = self._codebook_host.ctypes.data
         if self.bits == 6:
             s.stage2_packed = self.stage2_packed.data_ptr()
@@ -197,6 +208,34 @@ class QuantLinear(nn.Module):
         self._layer = self._make_layer() if self.packed.is_cuda else None
         self._bias_cache = {}
 
+    # Tensors whose addresses the kernel view holds, and the derived ones
+    # among them (plain attributes, moved by _apply).
+    _KERNEL_TENSORS = frozenset((
+        "packed", "scale", "gmin", "dq_scale_codes", "dq_scale_meta", "dq_gmin_codes", "dq_gmin_meta", "codebook",
+        "stage2_packed", "stage2_scale", "stage2_gmin", "outlier_row", "outlier_col", "outlier_delta", "bias",
+        "outlier_row_ptr", "tile_outliers", "outlier_colsorted"))
+    _DERIVED = ("outlier_row_ptr", "tile_outliers", "outlier_colsorted")
+
+    def __setattr__(self, name, value):
+        super().__setattr__(name, value)
+        # a reassigned tensor (e.g. a loader setting a buffer) gets a view on
+        # its new address; in-place updates keep their address
+        if name in QuantLinear._KERNEL_TENSORS and self.__dict__.get("_view_tracking", False):
+            self._rebuild_cache()
+
+    def _set_tensors(self, tensors: dict) -> None:
+        """Reassign several kernel tensors (buffers or derived) at once and
+        rebuild the view once."""
+        for n, v in tensors.items():
+            if n in self._buffers:
+                self._buffers[n] = v
+            else:
+                self.__dict__[n] = v
+        self._rebuild_cache()
+
+    def _kernel_tensor(self, name: str) -> Optional[torch.Tensor]:
+        return self._buffers[name] if name in self._buffers else self.__dict__.get(name)
+
     # Buffers the kernels read with a fixed element type. Module-wide casts
     # (`.half()`, `.to(torch.bfloat16)`) convert every floating buffer; these
     # are cast back so the kernel view keeps reading them as it expects (the
@@ -210,6 +249,10 @@ class QuantLinear(nn.Module):
 
     def _apply(self, fn, recurse=True):
         result = super()._apply(fn, recurse=recurse)
+        for name in self._DERIVED:
+            t = self.__dict__.get(name)
+            if t is not None:
+                self.__dict__[name] = fn(t)
         for name, dt in self._FIXED_DTYPES.items():
             b = self._buffers.get(name)
             if b is not None and b.dtype != dt:
