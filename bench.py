@@ -19,22 +19,28 @@ the width it needs; the first launch of a replay reads a resident input), as
 every linear of a decoder layer does.
 
 Alongside it (extra keys of the same JSON line):
-  * "roofline"     - the decode kernel: algorithmic bytes of a step's launches /
-                     the sum of their average durations (HIP events around
-                     graph replays of each launch over the copies), vs 8 TB/s;
-  * "decode_cfg5"  - the same decode step on BASELINE config 5's 70B layer
-                     (its 8/4/2-bit mix), 3 rotating copies (1.4 GB);
-  * "prefill"      - BASELINE config 4: gate/up/down at M=2048, 8-bit NF8 + DQ
-                     and 6-bit RVQ, 2*M*N*K flops / GPU time vs 2.5 PFLOP/s,
-                     through QuantLinear (dequantize into a workspace +
-                     hipBLASLt GEMM) and, as "fused_kernel", through the
-                     fused MFMA kernel (the same call without a workspace);
-  * "quantize"     - BASELINE config 5's GPU GOAP quantize (28672x8192) through
-                     the public API, wall time, with the oracle CPU codec timed
-                     on a slice;
-  * "cpu_baseline" - the reference CPU fallback forward (bf16 dequant + F.linear,
-                     modules.py:752-804, 924-940), restated in oracle/, timed
-                     on this host's cores for one layer forward at M=1.
+  * "roofline"       - the decode kernel: algorithmic bytes of a step's launches /
+                       the sum of their average durations (HIP events around
+                       graph replays of each launch over the copies), vs 8 TB/s;
+  * "decode_drop_in" - the same step as a caller of the reference API runs it:
+                       one QuantLinear.forward per linear, 7 launches
+                       ("decode_grouped" with --ungrouped);
+  * "cfg1"           - BASELINE config 1: the 4096x4096 linear by itself at
+                       M = 1 and 16, each line with the reference CPU fallback
+                       forward of the same layer timed beside it;
+  * "decode_cfg5"    - the same decode step on BASELINE config 5's 70B layer
+                       (its 8/4/2-bit mix), 3 rotating copies (1.4 GB);
+  * "prefill"        - BASELINE config 4: gate/up/down at M=2048, 8-bit NF8 + DQ
+                       and 6-bit RVQ, 2*M*N*K flops / GPU time vs 2.5 PFLOP/s,
+                       through QuantLinear.forward (the fused dequant-into-LDS
+                       MFMA kernel), with dequantize + hipBLASLt GEMM beside it
+                       as "library_reference";
+  * "quantize"       - BASELINE config 5's GPU GOAP quantize (28672x8192) through
+                       the public API, wall time, with the oracle CPU codec timed
+                       on the same full weight;
+  * "cpu_baseline"   - the reference CPU fallback forward (bf16 dequant + F.linear,
+                       modules.py:752-804, 924-940), restated in oracle/, timed
+                       on this host's cores for one layer forward at M=1.
 Synthetic seeded weights/activations (tests/golden/recipes.py).
 """
 from __future__ import annotations
@@ -82,10 +88,13 @@ def layer_bytes(ql, M: int) -> int:
 
 
 def clone_layer(ql):
-    """A second QuantLinear over fresh copies of the same buffers."""
+    """A second QuantLinear over fresh copies of the same buffers and derived
+    outlier tables."""
     import copy
     c = copy.copy(ql)
     c._buffers = {k: (v.clone() if v is not None else None) for k, v in ql._buffers.items()}
+    for name in ql._DERIVED:
+        c.__dict__[name] = ql.__dict__[name].clone()
     c._rebuild_cache()
     return c
 
@@ -142,15 +151,25 @@ def run_unit(layer, idx, xs, live=None):
     return ys
 
 
-def bench_decode(args, linears, opts_of, n_copies, steps, warmup, kernel_reps, sigma=0.02, seed0=1000):
-    import recipes
+def build_copies(linears, opts_of, n_copies, sigma=0.02, seed0=1000):
+    """A decoder layer and n_copies - 1 clones of it (rotated through so no
+    step finds its weights in the 256 MB MALL)."""
     torch.cuda.synchronize()
     base = build_decode_layer(linears, opts_of, sigma, seed0)
-    copies = [base] + [[(n, clone_layer(q)) for n, q in base] for _ in range(n_copies - 1)]
+    return [base] + [[(n, clone_layer(q)) for n, q in base] for _ in range(n_copies - 1)]
+
+
+def bench_decode(args, linears, opts_of, n_copies, steps, warmup, kernel_reps, sigma=0.02, seed0=1000,
+                 copies=None, units=None):
+    import recipes
+    if copies is None:
+        copies = build_copies(linears, opts_of, n_copies, sigma, seed0)
+    base = copies[0]
     widths = sorted({k for _, _, k in linears})
     xs = {k: recipes.activations(1, k).cuda() for k in widths}
     step_bytes = sum(layer_bytes(q, 1) for _, q in base)
-    units = SINGLE_UNITS if args.ungrouped else GROUPED_UNITS
+    if units is None:
+        units = SINGLE_UNITS if args.ungrouped else GROUPED_UNITS
     stream = torch.cuda.Stream()
     C = len(copies)
     full, rem = divmod(steps, C)
@@ -193,7 +212,66 @@ def bench_decode(args, linears, opts_of, n_copies, steps, warmup, kernel_reps, s
     step_gpu_ms = sum(a.elapsed_time(b) for a, b, _ in evs) / steps
     kern = unit_kernel_time(copies, xs, stream, units, reps=kernel_reps)
     return dict(ms_per_step=ms_per_step, value=value, step_bytes=step_bytes, kern=kern,
-                base=base, xs=xs, step_gpu_us=step_gpu_ms * 1e3, units=units)
+                base=base, xs=xs, step_gpu_us=step_gpu_ms * 1e3, units=units, copies=copies)
+
+
+def bench_single(copies, idx: int, M: int, reps: int):
+    """One linear of the layer by itself (BASELINE config 1 is the layer's
+    4096x4096 q shape): a graph holding its forward on every copy back to
+    back at M tokens, replayed `reps` times between HIP events on the launch
+    stream. Per-launch average (dispatch gap included)."""
+    import recipes
+    q0 = copies[0][idx][1]
+    x = recipes.activations(M, q0.in_features, seed=M).cuda()
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for layer in copies:
+            layer[idx][1](x)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for layer in copies:
+                layer[idx][1](x)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * len(copies))
+    nb = layer_bytes(q0, M)
+    return {"M": M, "bytes": nb, "us": round(us, 2), "GBps": round(nb / (us * 1e-6) / 1e9, 1),
+            "frac_of_hbm_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def cpu_forward_baseline(ql, M: int, budget_s: float):
+    """The reference CPU fallback forward (oracle restatement: bf16 dequant
+    + F.linear, modules.py:752-804, 924-940) of one linear at M tokens,
+    timed on this host's cores (median of up to 10 runs within budget_s)."""
+    import recipes
+    from oracle import codec_ref as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    qt = ql.to_quantized_tensor()
+    q = dict(packed=qt.packed, scale=qt.scale, gmin=qt.gmin, outlier_idx=qt.outlier_idx,
+             outlier_val=qt.outlier_val, dq_scale_codes=qt.dq_scale_codes, dq_scale_meta=qt.dq_scale_meta,
+             dq_gmin_codes=qt.dq_gmin_codes, dq_gmin_meta=qt.dq_gmin_meta, codebook=qt.codebook,
+             _meta=dict(bits=qt.bits, group_size=qt.group_size, rows=qt.rows, cols=qt.cols,
+                        padded_cols=qt.padded_cols, n_groups=qt.n_groups, orig_dtype=qt.orig_dtype))
+    bufs = dict(outlier_row=ql.outlier_row.cpu().numpy(), outlier_col=ql.outlier_col.cpu().numpy(),
+                outlier_delta=ql.outlier_delta.cpu().numpy())
+    x = recipes.activations(M, ql.in_features, seed=M)
+    O.quantlinear_forward_cpu(q, bufs, x)  # warmup
+    times, t_start = [], time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 10):
+        t0 = time.perf_counter()
+        O.quantlinear_forward_cpu(q, bufs, x)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    nb = layer_bytes(ql, M)
+    return {"value": round(nb / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "us": round(med * 1e6, 1), "sample": f"{len(times)} CPU forwards at M={M} (median)"}
 
 
 def unit_kernel_time(copies, xs, stream, units, reps: int):
@@ -261,15 +339,26 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
 
 
-def _forward_fused(q, x):
-    """ts_qlinear_forward without a workspace: the fused MFMA prefill kernel."""
+def _forward_gemm(q, x):
+    """ts_qlinear_forward with a workspace: dequantize into it + one hipBLASLt
+    GEMM (the library reference for the fused kernel)."""
     import ctypes
     from tensorshrink_amd import _lib as L
+    lib = L.load()
     y = torch.empty(x.shape[0], q.out_features, dtype=x.dtype, device=x.device)
+    n = lib.ts_forward_workspace_bytes(ctypes.byref(q._layer), x.shape[0])
+    ws = _WS.get(n)
+    if ws is None:
+        _WS.clear()
+        ws = _WS[n] = torch.empty(n, dtype=torch.uint8, device=x.device)
     dt = L.dtype_code(x.dtype)
-    L.check(L.load().ts_qlinear_forward(ctypes.byref(q._layer), x.data_ptr(), x.shape[0], q.in_features, dt,
-                                        y.data_ptr(), q.out_features, dt, None, None, 0, L.stream_ptr()), "fused")
+    L.check(lib.ts_qlinear_forward(ctypes.byref(q._layer), x.data_ptr(), x.shape[0], q.in_features, dt,
+                                   y.data_ptr(), q.out_features, dt, None, ws.data_ptr(), n, L.stream_ptr()),
+            "dequant + gemm")
     return y
+
+
+_WS: dict = {}
 
 
 def bench_prefill(args):
@@ -310,9 +399,13 @@ def bench_prefill(args):
                     "per_linear_us": {n: round(sum(t) / len(t) * 1e3, 1) for n, t in times.items()}}
 
         r = timed(lambda q, x: q(x))
-        r["path"] = "QuantLinear: dequantize into a workspace + hipBLASLt GEMM"
-        r["fused_kernel"] = timed(_forward_fused)
+        r["path"] = ("QuantLinear.forward: the fused dequant-into-LDS MFMA kernel (ts::prefill_kernel, "
+                     "256x256 tiles, 8 waves)")
+        lib_ref = timed(_forward_gemm)
+        lib_ref["path"] = "library reference: dequantize into a workspace + one hipBLASLt GEMM"
+        r["library_reference"] = lib_ref
         res[f"{bits}bit"] = r
+        _WS.clear()
         del lins, xs
         torch.cuda.empty_cache()
     return res
@@ -325,8 +418,8 @@ def bench_quantize(args):
     host numpy arrays, as the reference's does). Wall time per call with the
     weight resident on the GPU; algorithmic bytes = read N*K*2 + write packed
     + scale/gmin + outliers (i32 index + fp16 value). The reference CPU codec,
-    restated in oracle/ (libstdc++ top-k + numpy), is timed on a 2048-row
-    slice of the same weight on this host's cores."""
+    restated in oracle/ (libstdc++ top-k + numpy), is timed once on the same
+    full weight on this host's cores."""
     import numpy as np
     import recipes
     import tensorshrink_amd as ts
@@ -351,17 +444,15 @@ def bench_quantize(args):
            "ms": round(med * 1e3, 2), "bytes": nbytes, "GBps": round(nbytes / med / 1e9, 2),
            "frac_of_hbm_peak": round(nbytes / med / 1e9 / HBM_PEAK_GBS, 5)}
     if not args.no_cpu:
-        rows = 2048
-        ws = w[:rows].cpu()
+        wc = w.cpu()
         torch.set_num_threads(os.cpu_count() or 1)
         t0 = time.perf_counter()
-        O.quantize(ws, bits=4, group_size=gs, outlier_frac=frac)
+        O.quantize(wc, bits=4, group_size=gs, outlier_frac=frac)
         t = time.perf_counter() - t0
-        sb = rows * K * 2 + rows * K // 2 + 2 * rows * (K // gs) * 2 + int(rows * K * frac) * 6
-        res["cpu_baseline"] = {"value": round(sb / t / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+        res["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
                                "kind": "port", "ms": round(t * 1e3, 1),
-                               "sample": f"oracle CPU quantize of rows 0..{rows - 1} of the same weight "
-                                         f"({rows}x{K}), one call"}
+                               "sample": f"oracle CPU quantize of the same full {N}x{K} weight (k = {k}), one call"}
+        del wc
     del w
     torch.cuda.empty_cache()
     return res
@@ -430,6 +521,7 @@ def main():
     ap.add_argument("--no-decode70b", action="store_true")
     ap.add_argument("--quantize-reps", type=int, default=3)
     ap.add_argument("--copy-calib", action="store_true", help="only run the plain-copy PMC calibration")
+    ap.add_argument("--prefill-only", action="store_true", help="only the prefill lines (for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build targets a single MI355X and has no multi-GPU path "
@@ -440,12 +532,33 @@ def main():
     if args.copy_calib:
         copy_calibration()
         return
+    if args.prefill_only:
+        print(json.dumps({"prefill": bench_prefill(args)}), flush=True)
+        return
     import recipes
     opts = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
     log("decode: building layers")
+    copies = build_copies(recipes.LLAMA3_8B_LINEARS, lambda name: opts, args.copies)
     dec = bench_decode(args, recipes.LLAMA3_8B_LINEARS, lambda name: opts, args.copies, args.steps, args.warmup,
-                       args.kernel_reps)
+                       args.kernel_reps, copies=copies)
     kern = dec["kern"]
+    # the drop-in path: one QuantLinear.forward per linear, 7 launches a step
+    alt_units = GROUPED_UNITS if args.ungrouped else SINGLE_UNITS
+    alt = bench_decode(args, recipes.LLAMA3_8B_LINEARS, lambda name: opts, args.copies, min(args.steps, 30),
+                       min(args.warmup, 10), args.kernel_reps, copies=copies, units=alt_units)
+    alt_line = {"launches_per_step": len(alt_units), "us_per_step": round(alt["ms_per_step"] * 1e3, 2),
+                "GBps": round(alt["value"], 1), "frac_of_hbm_peak": round(alt["value"] / HBM_PEAK_GBS, 4),
+                "step_gpu_us": round(alt["step_gpu_us"], 2), "per_launch_isolated": alt["kern"]}
+    log(f"decode ({len(alt_units)} launches/step): {alt_line['us_per_step']} us/step, {alt_line['GBps']} GB/s")
+    # the 4096x4096 4-bit NF4 + DQ linear by itself (the
+    # layer's q), M = 1 and 16, with the reference CPU fallback beside it
+    cfg1 = {"workload": "BASELINE config 1: single QuantLinear 4096x4096, 4-bit NF4 + double quant, group 128, "
+                        "outlier_frac 0.001; one launch per forward, 10 rotating copies",
+            "lines": [bench_single(copies, 0, M, args.kernel_reps * 3) for M in (1, 16)]}
+    if not args.no_cpu:
+        for line in cfg1["lines"]:
+            line["cpu_baseline"] = cpu_forward_baseline(copies[0][0][1], line["M"], min(args.cpu_budget, 8.0))
+    log(f"cfg1: {cfg1['lines']}")
     k_us = sum(v["us"] for v in kern.values())
     achieved = dec["step_bytes"] / (dec["step_gpu_us"] * 1e-6) / 1e9
     log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s; GPU {dec['step_gpu_us']:.1f} "
@@ -510,6 +623,8 @@ def main():
                      "isolated_launch_us_per_layer": round(k_us, 2),
                      "per_launch_isolated": kern,
                      "traffic_per_launch": traffic["per_launch_bytes"] if traffic else None},
+        "decode_drop_in" if not args.ungrouped else "decode_grouped": alt_line,
+        "cfg1": cfg1,
         "decode_cfg5": d70,
         "prefill": pre,
         "quantize": quant,

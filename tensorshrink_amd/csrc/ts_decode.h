@@ -22,8 +22,9 @@
 //         y += s[n,g] * (x . cb[c]) + gmin[n,g] * (x . 1)
 //     with both dot products on the matrix core and s/gmin in float32
 //     (rebuilt from double-quant codes in-register, modules.py:573-579).
-//   * x at M = 1 comes in one 16-byte load per lane and batch and reaches the
-//     MFMA's A operand through DPP row broadcasts (no LDS); at M > 1 it is
+//   * x at M = 1 comes in one 16-byte load per lane and batch, is written to
+//     a wave-private LDS slot and read back per MFMA with the 16 lanes of a
+//     row on one address (a broadcast read, no VALU); at M > 1 it is
 //     staged once per workgroup in LDS when M*K fits, else read per MFMA from
 //     global memory, with two 16-row tiles per workgroup sharing each
 //     fragment when the launch is large.
@@ -100,46 +101,10 @@ struct DecodeGroup {
 };
 
 constexpr size_t DEC_XLDS_MAX = 64 * 1024;  // activations staged in LDS up to this size
-enum { XM_GLOBAL = 0, XM_DMA = 1, XM_REG = 2, XM_DPP = 3 };
+enum { XM_GLOBAL = 0, XM_DMA = 1, XM_REG = 2, XM_SLOT = 3 };
 // 16-byte x chunks per thread with XM_REG: 4 with 8 or 16 waves (x up to
 // 32 / 64 KB: a 14336- / 28672-wide row at M = 1), else 2.
 constexpr int xreg_chunks(int w) { return w >= 8 ? 4 : 2; }
-
-// Lane S of each 16-lane row of the wave, to every lane of that row (DPP
-// row_newbcast; S must be a constant once the caller's loops are unrolled).
-template <int S>
-TS_DEV uint32_t dpp_row_bcast(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + S, 0xf, 0xf, true);
-}
-template <int S>
-TS_DEV ts_u32x4 row_bcast_(ts_u32x4 v) {
-  return ts_u32x4{dpp_row_bcast<S>(v.x), dpp_row_bcast<S>(v.y), dpp_row_bcast<S>(v.z), dpp_row_bcast<S>(v.w)};
-}
-template <int S>
-TS_DEV ts_u32x2 row_bcast_(ts_u32x2 v) {
-  return ts_u32x2{dpp_row_bcast<S>(v.x), dpp_row_bcast<S>(v.y)};
-}
-template <typename V>
-TS_DEV V row_bcast(V v, int s) {
-  switch (s) {
-    case 0: return row_bcast_<0>(v);
-    case 1: return row_bcast_<1>(v);
-    case 2: return row_bcast_<2>(v);
-    case 3: return row_bcast_<3>(v);
-    case 4: return row_bcast_<4>(v);
-    case 5: return row_bcast_<5>(v);
-    case 6: return row_bcast_<6>(v);
-    case 7: return row_bcast_<7>(v);
-    case 8: return row_bcast_<8>(v);
-    case 9: return row_bcast_<9>(v);
-    case 10: return row_bcast_<10>(v);
-    case 11: return row_bcast_<11>(v);
-    case 12: return row_bcast_<12>(v);
-    case 13: return row_bcast_<13>(v);
-    case 14: return row_bcast_<14>(v);
-    default: return row_bcast_<15>(v);
-  }
-}
 
 template <bool BF16>
 TS_DEV uint32_t pack2(float lo, float hi) {
@@ -184,7 +149,7 @@ TS_DEV uint32_t half_of(const uint32_t* d, int i) { return (d[i >> 1] >> (16 * (
 // workgroup fills a CU (16 waves); with fewer waves per workgroup several
 // workgroups share the CU's LDS and get fewer copies.
 constexpr int dec_rep(int rep, int w) { return rep >= 32 ? (w >= 16 ? 32 : (w >= 8 ? 16 : 4)) : rep; }
-// With x in registers (XM_DPP) the LDS holds only the tables: four 4-wave
+// With x in per-wave slots (XM_SLOT) the LDS holds the tables and 1 KB per wave: four 4-wave
 // workgroups per CU fit 16 copies each.
 constexpr int dec_rep_x(int rep, int w, int xm) { return (xm == 3 && rep >= 32 && w == 4) ? 16 : dec_rep(rep, w); }
 
@@ -212,12 +177,12 @@ struct DecGeom {
 // with direct global->LDS loads. XM_REG keeps the compiler's wait counts
 // exact, so a wave computes its first batch while the second is in flight;
 // with direct-to-LDS loads pending the compiler treats the load counter as
-// out of order and its first wait drains everything. XM_DPP (M = 1): no LDS
-// staging; each batch brings its x columns in one load per lane (CPM
-// columns), lane 16 q + s holding the chunk that MFMA (u, j) = (s / NMF,
-// s % NMF) of lane group q needs, and a DPP row broadcast of lane s hands it
-// to all 16 lanes of row q. This takes the x operand off the LDS, which the code-table lookups
-// already keep busy.
+// out of order and its first wait drains everything. XM_SLOT (M = 1): no
+// workgroup staging; each batch brings its x columns in one load per lane
+// (CPM columns), lane 16 q + s holding the chunk that MFMA (u, j) = (s / NMF,
+// s % NMF) of lane group q needs; the wave writes them to its own LDS slot
+// and each MFMA reads its chunk back on one address per 16-lane row (DPP row
+// broadcasts of the chunks, the earlier design, cost 16 VALU moves per group).
 // AL: the row's group count is a multiple of U, so every batch starts on a
 // multiple of U in the row-major (row, group) metadata arrays and its U codes
 // / scales come in one aligned vector load.
@@ -229,7 +194,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   constexpr int NT = 64 * W;
   constexpr bool LOOP = NB == 0;
   constexpr int R = dec_rep_x(REP, W, XM);  // table copies
-  constexpr bool XLDS = XM != XM_GLOBAL && XM != XM_DPP;
+  constexpr bool XLDS = XM != XM_GLOBAL && XM != XM_SLOT;
   extern __shared__ __align__(16) unsigned char smem[];
   using Geo = DecGeom<BITS, GS, RVQ>;
   constexpr int GB = Geo::GB, LB = Geo::LB, GB2 = Geo::GB2, LB2 = Geo::LB2;
@@ -285,6 +250,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   sp += RT * W * 64 * 4 * 4;
   float* cbs = reinterpret_cast<float*>(sp);       // [256] staged codebook
   sp += 256 * 4;
+  // XM_SLOT: each wave's x slot (64 lanes x 16 bytes)
+  uint16_t* xw = reinterpret_cast<uint16_t*>(sp) + wave * 512;
+  if constexpr (XM == XM_SLOT) sp += W * 1024;
   uint16_t* xs = reinterpret_cast<uint16_t*>(sp);  // [M][K] staged activations (XLDS)
 
   // ---- per-wave share of every tile ----------------------------------------
@@ -313,7 +281,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     int split;                      // groups u < split use the first super-group
     uint32_t s2s[RVQ ? (AL ? NW16 : U) : 1], s2g[RVQ ? (AL ? NW16 : U) : 1];  // RVQ stage-2 f16 bits
     uint32_t live;                  // bit u set when group u of the batch exists
-    ts_u32x4 xv;                    // XM_DPP: this lane's x chunk of the batch
+    ts_u32x4 xv;                    // XM_SLOT: this lane's x chunk of the batch
   };
 
   // TQ (4-byte quarter-groups: 2-bit group 64, 4-bit group 32): each lane
@@ -323,24 +291,24 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // two v_permlane32_swap + two v_permlane16_swap), which leaves lane q with
   // quarter q of groups gb + 4 h .. + 3: one 16-byte load instead of four
   // 4-byte ones.
-  auto load_batch = [&](int64_t tile, int b, Batch& B) {
+  auto load_batch_of = [&](const DecodeArgs& A, int64_t tile, int b, Batch& B) {
     const int gb = g_lo + b * U;
     const bool any = gb < g_hi;
     // a dead batch (past the wave's run) reads the tile's first row at one
     // address per load: one cache line, never used
-    const int64_t r = any ? min(tile * 16 + n, a.N - 1) : min(tile * 16, a.N - 1);
-    const uint8_t* wp = a.packed + r * a.pstride + (any ? q * LB : 0);
+    const int64_t r = any ? min(tile * 16 + n, A.N - 1) : min(tile * 16, A.N - 1);
+    const uint8_t* wp = A.packed + r * A.pstride + (any ? q * LB : 0);
     const int gb0 = any ? gb : g_lo;  // a dead batch re-reads the wave's first groups
-    if constexpr (XM == XM_DPP) {
+    if constexpr (XM == XM_SLOT) {
       // chunk of group gb0 + s / NMF, columns (NMF q + s % NMF) * CPM .. + CPM of it
       const int sl = lane & 15;
       const int col = (gb0 + sl / NMF) * GS + (NMF * q + sl % NMF) * CPM;
-      const bool use = sl < U * NMF && col < a.cols;
+      const bool use = sl < U * NMF && col < A.cols;
       if constexpr (CPM == 8) {
-        const ts_u32x4 v = ts_ld16(a.x + min(col, (int)a.cols - 8));
+        const ts_u32x4 v = ts_ld16(A.x + min(col, (int)A.cols - 8));
         B.xv = use ? v : ts_u32x4{0u, 0u, 0u, 0u};
       } else {
-        const ts_u32x2 v = ts_ld8(a.x + min(col, (int)a.cols - 4));
+        const ts_u32x2 v = ts_ld8(A.x + min(col, (int)A.cols - 4));
         B.xv = use ? ts_u32x4{v.x, v.y, 0u, 0u} : ts_u32x4{0u, 0u, 0u, 0u};
       }
     }
@@ -353,7 +321,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       gg[u] = live ? gb + u : gb0;
     }
     if constexpr (TQ) {
-      const uint8_t* rowp = a.packed + r * a.pstride;
+      const uint8_t* rowp = A.packed + r * A.pstride;
 #pragma unroll
       for (int h = 0; h < U / 4; ++h) {
         const int gq = gb + 4 * h + q;
@@ -367,59 +335,61 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     if constexpr (RVQ) {
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        B.w2[u] = load_bytes<LB2>(a.s2packed + r * a.s2stride + q * LB2 + (int64_t)gg[u] * GB2);
+        B.w2[u] = load_bytes<LB2>(A.s2packed + r * A.s2stride + q * LB2 + (int64_t)gg[u] * GB2);
       if constexpr (AL) {
-        const Bytes<2 * U> vs = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.s2scale + rowg + gb0));
-        const Bytes<2 * U> vg = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.s2gmin + rowg + gb0));
+        const Bytes<2 * U> vs = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(A.s2scale + rowg + gb0));
+        const Bytes<2 * U> vg = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(A.s2gmin + rowg + gb0));
 #pragma unroll
         for (int i = 0; i < NW16; ++i) { B.s2s[i] = vs.d[i]; B.s2g[i] = vg.d[i]; }
       } else {
 #pragma unroll
-        for (int u = 0; u < U; ++u) { B.s2s[u] = a.s2scale[rowg + gg[u]]; B.s2g[u] = a.s2gmin[rowg + gg[u]]; }
+        for (int u = 0; u < U; ++u) { B.s2s[u] = A.s2scale[rowg + gg[u]]; B.s2g[u] = A.s2gmin[rowg + gg[u]]; }
       }
     }
     if constexpr (DQ) {
       if constexpr (AL) {
-        const Bytes<U> vs = load_bytes<U>(a.dqsc + rowg + gb0);
-        const Bytes<U> vg = load_bytes<U>(a.dqgc + rowg + gb0);
+        const Bytes<U> vs = load_bytes<U>(A.dqsc + rowg + gb0);
+        const Bytes<U> vg = load_bytes<U>(A.dqgc + rowg + gb0);
 #pragma unroll
         for (int i = 0; i < NW8; ++i) { B.sc[i] = vs.d[i]; B.gc[i] = vg.d[i]; }
       } else {
 #pragma unroll
-        for (int u = 0; u < U; ++u) { B.sc[u] = a.dqsc[rowg + gg[u]]; B.gc[u] = a.dqgc[rowg + gg[u]]; }
+        for (int u = 0; u < U; ++u) { B.sc[u] = A.dqsc[rowg + gg[u]]; B.gc[u] = A.dqgc[rowg + gg[u]]; }
       }
       // The batch's live groups are consecutive, so they span at most two
       // super-groups (dq_gs >= U is checked on the host).
       const int nlive = max(1, min(U, g_hi - gb));
       const uint32_t f0 = (uint32_t)(rowg + gb0);
-      const uint32_t sup0 = f0 / a.dq_gs;
-      const uint32_t sup1 = (f0 + (uint32_t)(any ? nlive - 1 : 0)) / a.dq_gs;
-      B.split = (int)min((uint32_t)U, (sup0 + 1) * a.dq_gs - f0);
+      const uint32_t sup0 = f0 / A.dq_gs;
+      const uint32_t sup1 = (f0 + (uint32_t)(any ? nlive - 1 : 0)) / A.dq_gs;
+      B.split = (int)min((uint32_t)U, (sup0 + 1) * A.dq_gs - f0);
       // super-groups sup0 and sup0 + 1 in one 8-byte buffer load per array
       // (raw: nothing here consumes it). sup1 is sup0 or sup0 + 1, and when
       // it is sup0 every live group is below split, so B is never read (past
       // the last super-group the buffer load returns zeros).
       (void)sup1;
-      const ts_u32x2 sm = ts_bld8(ts_rsrc(a.dqsm, a.dqm_bytes), 4u * sup0);
-      const ts_u32x2 gv = ts_bld8(ts_rsrc(a.dqgm, a.dqm_bytes), 4u * sup0);
+      const ts_u32x2 sm = ts_bld8(ts_rsrc(A.dqsm, A.dqm_bytes), 4u * sup0);
+      const ts_u32x2 gv = ts_bld8(ts_rsrc(A.dqgm, A.dqm_bytes), 4u * sup0);
       B.smA = sm.x;
       B.smB = sm.y;
       B.gmA = gv.x;
       B.gmB = gv.y;
     } else {
       if constexpr (AL) {
-        const Bytes<2 * U> vs = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.scale + rowg + gb0));
-        const Bytes<2 * U> vg = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(a.gmin + rowg + gb0));
+        const Bytes<2 * U> vs = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(A.scale + rowg + gb0));
+        const Bytes<2 * U> vg = load_bytes<2 * U>(reinterpret_cast<const uint8_t*>(A.gmin + rowg + gb0));
 #pragma unroll
         for (int i = 0; i < NW16; ++i) { B.sc[i] = vs.d[i]; B.gc[i] = vg.d[i]; }
       } else {
 #pragma unroll
-        for (int u = 0; u < U; ++u) { B.sc[u] = a.scale[rowg + gg[u]]; B.gc[u] = a.gmin[rowg + gg[u]]; }
+        for (int u = 0; u < U; ++u) { B.sc[u] = A.scale[rowg + gg[u]]; B.gc[u] = A.gmin[rowg + gg[u]]; }
       }
       B.smA = B.smB = B.gmA = B.gmB = 0u;
       B.split = U;
     }
   };
+
+  auto load_batch = [&](int64_t tile, int b, Batch& B) { load_batch_of(a, tile, b, B); };
 
   // float32 (scale, gmin) of group u of a batch
   auto group_affine = [&](const Batch& B, int u, float& s_, float& gm_) {
@@ -437,6 +407,14 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   };
 
   auto compute_batch = [&](int b, const Batch& B, ts_f32x4& yacc) {
+    // M = 1: the batch's x chunks go to this wave's LDS slot once; each MFMA
+    // then reads its chunk back with the 16 lanes of a row on one address (a
+    // broadcast read), instead of moving it with DPP (VALU) per MFMA. Reads
+    // of the previous batch were issued before this write (in-order LDS).
+    if constexpr (XM == XM_SLOT) {
+      if constexpr (CPM == 8) *reinterpret_cast<ts_u32x4*>(xw + lane * 8) = B.xv;
+      else *reinterpret_cast<ts_u32x2*>(xw + lane * 4) = ts_u32x2{B.xv.x, B.xv.y};
+    }
     // the batch's code dwords per group (TQ: after the quarter transpose)
     uint32_t wt[TQ ? U : 1];
     if constexpr (TQ) {
@@ -471,8 +449,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
         // A-operand row n >= M only feeds output rows that are never stored,
         // so those lanes read row M - 1 (no predicate, one base per lane).
         if constexpr (CPM == 8) {
-          if constexpr (XM == XM_DPP) {
-            xa[j] = row_bcast(B.xv, u * NMF + j);
+          if constexpr (XM == XM_SLOT) {
+            xa[j] = *reinterpret_cast<const ts_u32x4*>(xw + (16 * q + u * NMF + j) * 8);
           } else if constexpr (XLDS) {
             xa[j] = *reinterpret_cast<const ts_u32x4*>(xrow_lds + col);
           } else {
@@ -481,8 +459,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
           }
         } else {
           ts_u32x2 v;
-          if constexpr (XM == XM_DPP) {
-            v = row_bcast(ts_u32x2{B.xv.x, B.xv.y}, u * NMF + j);
+          if constexpr (XM == XM_SLOT) {
+            v = *reinterpret_cast<const ts_u32x2*>(xw + (16 * q + u * NMF + j) * 4);
           } else if constexpr (XLDS) {
             v = *reinterpret_cast<const ts_u32x2*>(xrow_lds + col);
           } else {
@@ -539,8 +517,10 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
         s2_ = ts_h2f((uint16_t)(AL ? half_of(B.s2s, u) : B.s2s[u]));
         g2_ = ts_h2f((uint16_t)(AL ? half_of(B.s2g, u) : B.s2g[u]));
       }
+      // M = 1 (XM_SLOT): only element 0 of lanes 0-15 (token 0) is stored
+      constexpr int NI = XM == XM_SLOT ? 1 : 4;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NI; ++i) {
         float v = yacc[i];
         v = __builtin_fmaf(s_, aw[i], v);
         v = __builtin_fmaf(gm_, ax[i], v);
@@ -805,6 +785,52 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     return;
   }
 
+  // ---- epilogue of one tile: reduce the waves' partials, outliers, bias, store
+  // The tile's outliers are added into this wave's own partials, which it has
+  // just written (a wave's LDS operations complete in order), so the single
+  // barrier before the cross-wave sum covers them too. Entry of token m, row
+  // nn: lane nn + 16 (m / 4), element m % 4 (the MFMA's D layout). rb: the
+  // partials buffer ([W][64][4]).
+  auto epilogue_of = [&](const DecodeArgs& A, int64_t t, const ts_f32x4& yv, uint64_t slot0, uint16_t bias_v,
+                         float* rb) {
+    *reinterpret_cast<ts_f32x4*>(rb + (wave * 64 + lane) * 4) = yv;
+    if (A.cap > 0) {
+      // slot = col | (row in tile) << 32 | f16 delta << 48; a zero delta (an
+      // unused slot) adds nothing and is skipped
+      float* rw = rb + wave * 64 * 4;
+      auto add_slot = [&](uint64_t v) {
+        const uint32_t dbits = (uint32_t)(v >> 48);
+        if (dbits == 0u) return;
+        const uint32_t col = (uint32_t)v, row = (uint32_t)(v >> 32) & 0xffffu;
+        const float d = ts_h2f((uint16_t)dbits);
+        for (int m = 0; m < A.M; ++m) {
+          const float xv = XLDS ? XT<BF16>::to_f(xs[m * A.K + col]) : XT<BF16>::to_f(A.x[(int64_t)m * A.ldx + col]);
+          atomicAdd(&rw[(row + 16 * (m >> 2)) * 4 + (m & 3)], xv * d);
+        }
+      };
+      if (tid < A.cap) add_slot(slot0);
+      for (int i = tid + NT; i < A.cap; i += NT) add_slot(A.slots[t * A.cap + i]);  // rare: > NT in a tile
+    }
+    ts_lds_barrier();
+    // the tile's 16 x 16 (token m, row nn) outputs: the thread that sums one
+    // over the waves also adds the bias and stores it
+    if (tid < 256) {
+      const int l = tid >> 2, i = tid & 3;
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) acc += rb[(w * 64 + l) * 4 + i];
+      const int m = 4 * (l >> 4) + i, nn = l & 15;
+      const int64_t r = t * 16 + nn;
+      if (m < A.M && r < A.N) {
+        if (A.bias_mul) acc += XT<BF16>::to_f(bias_v);
+        const int64_t off = (int64_t)m * A.ldy + r;
+        if (A.y_dtype == TS_F32) reinterpret_cast<float*>(A.y)[off] = acc;
+        else if (A.y_dtype == TS_BF16) reinterpret_cast<uint16_t*>(A.y)[off] = ts_f2bf(acc);
+        else reinterpret_cast<uint16_t*>(A.y)[off] = ts_f2h(acc);
+      }
+    }
+  };
+
   // The weight stream starts only now, after the workgroup's barriers: a
   // barrier behind it would wait until every wave had issued all its loads,
   // which under a full memory pipeline is most of the stream, and no wave
@@ -848,47 +874,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
   }
 
-  // ---- epilogue: reduce the waves' partials, outliers, bias, store ----------
-  // The tile's outliers are added into this wave's own partials, which it has
-  // just written (a wave's LDS operations complete in order), so the single
-  // barrier before the cross-wave sum covers them too. Entry of token m, row
-  // nn: lane nn + 16 (m / 4), element m % 4 (the MFMA's D layout).
-  *reinterpret_cast<ts_f32x4*>(red + (wave * 64 + lane) * 4) = yacc;
-  if (a.cap > 0) {
-    // slot = col | (row in tile) << 32 | f16 delta << 48; a zero delta (an
-    // unused slot) adds nothing and is skipped
-    float* rw = red + wave * 64 * 4;
-    auto add_slot = [&](uint64_t v) {
-      const uint32_t dbits = (uint32_t)(v >> 48);
-      if (dbits == 0u) return;
-      const uint32_t col = (uint32_t)v, row = (uint32_t)(v >> 32) & 0xffffu;
-      const float d = ts_h2f((uint16_t)dbits);
-      for (int m = 0; m < a.M; ++m) {
-        const float xv = XLDS ? XT<BF16>::to_f(xs[m * a.K + col]) : XT<BF16>::to_f(a.x[(int64_t)m * a.ldx + col]);
-        atomicAdd(&rw[(row + 16 * (m >> 2)) * 4 + (m & 3)], xv * d);
-      }
-    };
-    if (tid < a.cap) add_slot(slot0);
-    for (int i = tid + NT; i < a.cap; i += NT) add_slot(a.slots[sbase + i]);  // rare: > NT in a tile
-  }
-  ts_lds_barrier();
-  // the tile's 16 x 16 (token m, row nn) outputs: the thread that sums one
-  // over the waves also adds the bias and stores it
-  if (tid < 256) {
-    const int l = tid >> 2, i = tid & 3;
-    float acc = 0.f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) acc += red[(w * 64 + l) * 4 + i];
-    const int m = 4 * (l >> 4) + i, nn = l & 15;
-    const int64_t r = r0 + nn;
-    if (m < a.M && r < a.N) {
-      if (a.bias_mul) acc += XT<BF16>::to_f(bias_v);
-      const int64_t off = (int64_t)m * a.ldy + r;
-      if (a.y_dtype == TS_F32) reinterpret_cast<float*>(a.y)[off] = acc;
-      else if (a.y_dtype == TS_BF16) reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2bf(acc);
-      else reinterpret_cast<uint16_t*>(a.y)[off] = ts_f2h(acc);
-    }
-  }
+  epilogue_of(a, tile, yacc, slot0, bias_v, red);
 }
 
 template <int BITS, bool CB8, bool RVQ, int REP, int XM, int W, int RT>
@@ -900,6 +886,7 @@ inline size_t decode_smem(int M, int64_t K, bool xlds) {
   if (BITS == 8 && CB8) s += 256 * R * 4;
   s += (size_t)RT * W * 64 * 16;
   s += 256 * 4;
+  if (XM == XM_SLOT) s += (size_t)W * 1024;
   if (xlds) s += ((size_t)M * K * 2 + 1023) / 1024 * 1024;  // whole 1 KB chunks
   return s;
 }
@@ -917,7 +904,7 @@ inline int launch_decode_x(const DecodeGroup& g_in, hipStream_t st) {
     }
   }
   const DecodeArgs& a = g.a[0];
-  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, XM, W, RT>(a.M, a.K, XM != XM_GLOBAL && XM != XM_DPP);
+  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, XM, W, RT>(a.M, a.K, XM != XM_GLOBAL && XM != XM_SLOT);
   auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB, RT>;
   static std::once_flag flags[64];
   static bool ok[64];
@@ -981,10 +968,10 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   const DecShape sh = decode_shape(g.tile_end[g.n - 1], a.n_groups, UMAX);
   // x through registers when xreg_chunks(w) chunks per thread hold it
   auto xreg = [&](int w) { return xlds && (int64_t)a.M * a.K / 8 <= (int64_t)xreg_chunks(w) * 64 * w; };
-  // M = 1: x through DPP row broadcasts when a batch's (group, MFMA) pairs fit
+  // M = 1: x through per-wave LDS slots when a batch's (group, MFMA) pairs fit
   // the 16 lanes of a row
-  constexpr bool DPP_OK = UMAX * ((BITS == 8 && CB8) ? GS / 16 : GS / 32) <= 16;
-  const bool dpp = DPP_OK && a.M == 1;
+  constexpr bool SLOT_OK = UMAX * ((BITS == 8 && CB8) ? GS / 16 : GS / 32) <= 16;
+  const bool slot = SLOT_OK && a.M == 1;
   const bool one = (a.n_groups + UMAX - 1) / UMAX <= sh.W;  // one batch per wave
   // x from global memory at M > 1 with at least half a resident round of
   // waves: two row tiles per workgroup share each x fragment (4-bit codes),
@@ -1003,20 +990,20 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
 #define TS_DEC_ALL(DQV)                                                          \
   do {                                                                           \
     const bool alm = aligned(UMAX);                                              \
-    if constexpr (DPP_OK) {                                                      \
-      if (dpp && sh.ok && alm) {                                                 \
+    if constexpr (SLOT_OK) {                                                      \
+      if (slot && sh.ok && alm) {                                                 \
         if (sh.W == 4) {                                                         \
-          if (one) TS_DEC1(XM_DPP, DQV, true, 4, UMAX);                          \
-          TS_DEC(XM_DPP, DQV, true, 4, UMAX, false);                             \
+          if (one) TS_DEC1(XM_SLOT, DQV, true, 4, UMAX);                          \
+          TS_DEC(XM_SLOT, DQV, true, 4, UMAX, false);                             \
         }                                                                        \
         if (sh.W == 8) {                                                         \
-          if (one) TS_DEC1(XM_DPP, DQV, true, 8, UMAX);                          \
-          TS_DEC(XM_DPP, DQV, true, 8, UMAX, false);                             \
+          if (one) TS_DEC1(XM_SLOT, DQV, true, 8, UMAX);                          \
+          TS_DEC(XM_SLOT, DQV, true, 8, UMAX, false);                             \
         }                                                                        \
-        if (one) TS_DEC1(XM_DPP, DQV, true, 16, UMAX);                           \
-        TS_DEC(XM_DPP, DQV, true, 16, UMAX, false);                              \
+        if (one) TS_DEC1(XM_SLOT, DQV, true, 16, UMAX);                           \
+        TS_DEC(XM_SLOT, DQV, true, 16, UMAX, false);                              \
       }                                                                          \
-      if (dpp && alm) TS_DEC(XM_DPP, DQV, true, 16, UMAX, true);                 \
+      if (slot && alm) TS_DEC(XM_SLOT, DQV, true, 16, UMAX, true);                 \
     }                                                                            \
     if constexpr (RT2_OK) {                                                      \
       if (rt2) {                                                                 \

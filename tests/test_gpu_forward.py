@@ -432,3 +432,25 @@ def test_forward_quarter_group_codes(bits, gs, dq):
         err = max_rel_err(ql(x).float(), x.float() @ W.T)
         say("quarter groups", bits, gs, dq, M, err)
         assert err <= TOL, (M, err)
+
+
+@pytest.mark.slow
+def test_forward_group_persistent_schedule():
+    """Launches beyond one resident round of waves run the persistent decode
+    schedule (workgroups loop over tiles, refilling their batches across tile
+    boundaries): config 3's gate/up as one grouped launch (2 x 896 tiles x 4
+    waves) with a bias on one layer, against the digest-pinned weights, at
+    M = 1 (persistent) and 4 (the other schedule)."""
+    ts = _ts()
+    (gq, Wg), (uq, Wu) = _pinned(CFG3_NAMES[4]), _pinned(CFG3_NAMES[5])
+    torch.manual_seed(1)
+    uq.bias = (torch.randn(uq.out_features) * 0.1).to(torch.bfloat16).cuda()
+    for M in (1, 4):
+        x = recipes.activations(M, 4096, seed=40 + M).cuda()
+        yg, yu = ts.QuantLinear.forward_group([gq, uq], x)
+        for y, W, b, q in ((yg, Wg, None, gq), (yu, Wu, uq.bias, uq)):
+            ref = x.float() @ W.T + (b.float() if b is not None else 0)
+            err = max_rel_err(y.float(), ref)
+            say("persistent group", M, err)
+            assert err <= TOL, (M, err)
+            assert max_rel_err(y.float(), q(x).float()) <= 1e-3
