@@ -548,7 +548,8 @@ def main():
                        min(args.warmup, 10), args.kernel_reps, copies=copies, units=alt_units)
     alt_line = {"launches_per_step": len(alt_units), "us_per_step": round(alt["ms_per_step"] * 1e3, 2),
                 "GBps": round(alt["value"], 1), "frac_of_hbm_peak": round(alt["value"] / HBM_PEAK_GBS, 4),
-                "step_gpu_us": round(alt["step_gpu_us"], 2), "per_launch_isolated": alt["kern"]}
+                "step_gpu_us": round(alt["step_gpu_us"], 2), "per_launch_isolated": alt["kern"],
+                "traffic": (load_traffic(alt_units) or {}).get("bytes_per_step")}
     log(f"decode ({len(alt_units)} launches/step): {alt_line['us_per_step']} us/step, {alt_line['GBps']} GB/s")
     # the 4096x4096 4-bit NF4 + DQ linear by itself (the
     # layer's q), M = 1 and 16, with the reference CPU fallback beside it
