@@ -458,6 +458,40 @@ def bench_quantize(args):
     return res
 
 
+def bench_quantize_module(args):
+    """quantize_module over BASELINE config 5's layer (q/k/v/o, gate/up/down of
+    the 70B shape, fp16 CPU weights as a model holds them before it moves to
+    the GPU), NF4 + double quant (quantize_module's defaults), wall time with
+    one and with four top-k replay workers (the layers' heap replays then run
+    in parallel; results are identical)."""
+    import recipes
+    import tensorshrink_amd as ts
+    lins = recipes.LLAMA3_70B_LINEARS
+    ws = [recipes.gaussian_weight(n, k, 5200 + i, sigma=0.015) for i, (_, n, k) in enumerate(lins)]
+    nbytes = sum(w.numel() * 2 for w in ws)
+
+    def model():
+        m = torch.nn.Module()
+        for (name, n, k), w in zip(lins, ws):
+            lin = torch.nn.Linear(k, n, bias=False, dtype=torch.float16)
+            lin.weight.data = w
+            m.add_module(name, lin)
+        return m
+    res = {"workload": "quantize_module over the config-5 layer's 7 linears (855 M fp16 weights on the host), "
+                       "NF4 + double quant, group 128, outlier_frac 0.001", "bytes": nbytes}
+    for workers in (1, 4):
+        m = model()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ts.quantize_module(m, verbose=False, quantize_workers=workers, skip_name_patterns=())
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+        res[f"workers_{workers}"] = {"s": round(t, 3), "GBps": round(nbytes / t / 1e9, 2)}
+        del m
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(dec, budget_s: float):
     """Time the reference CPU fallback forward (oracle restatement) for one
     layer at M=1, on this host's cores, with the layer's own codes."""
@@ -590,6 +624,8 @@ def main():
         log("quantize: 28672x8192")
         quant = bench_quantize(args)
         log(f"quantize: {quant}")
+        quant["module"] = bench_quantize_module(args)
+        log(f"quantize_module: {quant['module']}")
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")

@@ -254,16 +254,103 @@ def _linspace(lo: float, hi: float, n: int, device) -> np.ndarray:
     return torch.linspace(lo, hi, n, device=device).cpu().numpy().astype(np.float32)
 
 
+class _Done:
+    """An already-computed top-k, with the interface of _Replay."""
+
+    def __init__(self, result):
+        self.result = result
+
+    def get(self):
+        return self.result
+
+
+def _k_of(n: int, outlier_frac: float) -> int:
+    return max(1, int(n * outlier_frac)) if outlier_frac > 0 else 0
+
+
+def topk_of(w: torch.Tensor, outlier_frac: float) -> Optional[Tuple[np.ndarray, np.ndarray]]:
+    """torch.topk(|w|, k) of a weight (indices, |w| values; k from
+    outlier_frac as quantize_tensor takes it), or None without outliers: the
+    part of a quantize that depends on the weight and outlier_frac only, so
+    the quantizes of one tensor at several bit widths can share it. Thread
+    safe; the host heap replay releases the GIL."""
+    w2d, _ = _to_2d(w)
+    n = w2d.shape[0] * w2d.shape[1]
+    k = _k_of(n, outlier_frac)
+    if not 0 < k < n:
+        return None
+    wg = _gpu_weight(w2d, _device())
+    ci, cv = _topk_candidates(wg, k)
+    del wg  # the replay needs only the host candidates
+    return _topk_select(ci, cv, n, k)
+
+
+class TopkPrefetch:
+    """topk_of() for a sequence of weights, computed ahead on a thread pool
+    of `workers` threads, at most 2 x workers weights ahead of the consumer.
+    Each weight's heap replay is sequential, but the replays of different
+    weights run in parallel (the replay releases the GIL). get(i) waits for
+    weight i's result; the pool holds a weight only until its top-k is done,
+    and shuts down after the last one (a consumer that stops early leaves at
+    most the window's bounded jobs to finish). With workers <= 1, get(i)
+    computes in the calling thread."""
+
+    def __init__(self, weights, outlier_frac: float, workers: int):
+        from concurrent.futures import ThreadPoolExecutor
+        self.ws = list(weights)
+        self.frac = outlier_frac
+        self.ex = ThreadPoolExecutor(max_workers=workers) if workers > 1 and len(self.ws) > 1 else None
+        self.window = 2 * max(1, workers)
+        self.fut = {}
+        self.next = 0
+        self._fill(0)
+
+    def _fill(self, i: int) -> None:
+        if self.ex is None:
+            return
+        while self.next < len(self.ws) and self.next < i + self.window:
+            self.fut[self.next] = self.ex.submit(topk_of, self.ws[self.next], self.frac)
+            self.ws[self.next] = None
+            self.next += 1
+
+    def get(self, i: int):
+        if self.ex is None:
+            w, self.ws[i] = self.ws[i], None
+            return topk_of(w, self.frac)
+        self._fill(i)
+        r = self.fut.pop(i).result()
+        self._fill(i + 1)
+        if not self.fut and self.next >= len(self.ws):
+            self.close()  # the last weight: release the pool's threads
+        return r
+
+    def close(self) -> None:
+        if self.ex is not None:
+            for f in self.fut.values():
+                f.cancel()
+            self.ex.shutdown(wait=True)
+            self.ex = None
+
+
 def _quantize_2d(wg: torch.Tensor, rows: int, cols: int, bits: int, group_size: int, k: int,
                  nf_quant: bool, companded: bool, double_quant: bool, dq_group_size: int,
-                 rng_device) -> dict:
-    """GPU GOAP quantize of a [rows, cols] device tensor; returns numpy fields."""
+                 rng_device, topk=None) -> dict:
+    """GPU GOAP quantize of a [rows, cols] device tensor; returns numpy fields.
+    `topk`: this weight's top-k from topk_of(), computed once for several
+    quantizes of it."""
     lib = L.lib()
     dev = wg.device
     st = L.stream_ptr()
     n = rows * cols
     replay = None
-    if 0 < k < n:
+    if 0 < k < n and topk is not None:
+        if topk[0].shape[0] != k:
+            raise ValueError("precomputed top-k does not match outlier_frac")
+        replay = _Done(topk)
+        nan = bool(np.isnan(topk[1]).any())
+        t = float(topk[1].min())  # the k-th largest |w| (NaN when a NaN is ranked in)
+        clamp = 1
+    elif 0 < k < n:
         ci, cv = _topk_candidates(wg, k)
         replay = _Replay(ci, cv, n, k)
         # The clamp threshold min(topk values) is the k-th largest |w|: every
@@ -366,11 +453,13 @@ def quantize_tensor(
     smooth_alpha: float = DEFAULT_SMOOTH_ALPHA,
     companded: bool = False,
     nf_quant: bool = False,
+    _topk=None,
 ) -> QuantizedTensor:
     """GOAP quantize of a weight tensor (ndim >= 2) on the GPU (codec.py:453-675).
 
     Same arguments, defaults and errors as the reference. The input may live
-    on the CPU or the GPU; the result holds host numpy arrays.
+    on the CPU or the GPU; the result holds host numpy arrays. (`_topk`, not
+    part of the reference's signature: this weight's topk_of() result.)
     """
     if bits not in (2, 4, 6, 8):
         raise ValueError("bits must be 2, 4, 6, or 8")
@@ -378,7 +467,7 @@ def quantize_tensor(
         if companded:
             raise ValueError("companded=True is not supported with bits=6 (RVQ)")
         return _quantize_rvq(w, group_size=group_size, outlier_frac=outlier_frac, double_quant=double_quant,
-                             dq_group_size=dq_group_size, smooth=smooth, smooth_alpha=smooth_alpha)
+                             dq_group_size=dq_group_size, smooth=smooth, smooth_alpha=smooth_alpha, _topk=_topk)
     if smooth:
         raise NotImplementedError("smooth=True is not covered by tensorshrink_amd")
     orig_dtype = str(w.dtype).replace("torch.", "")
@@ -387,9 +476,9 @@ def quantize_tensor(
     dev = _device()
     wg = _gpu_weight(w2d, dev)
     n = rows * cols
-    k = max(1, int(n * outlier_frac)) if outlier_frac > 0 else 0
+    k = _k_of(n, outlier_frac)
     f = _quantize_2d(wg, rows, cols, bits, group_size, k, nf_quant, companded, double_quant, dq_group_size,
-                     w.device)
+                     w.device, topk=_topk)
     return QuantizedTensor(
         orig_shape=orig_shape, orig_dtype=orig_dtype, bits=bits, group_size=group_size, rows=rows, cols=cols,
         padded_cols=f["padded_cols"], n_groups=f["n_groups"], packed=f["packed"], scale=f["scale"],
@@ -399,14 +488,14 @@ def quantize_tensor(
 
 
 def _quantize_rvq(w, group_size=DEFAULT_GROUP_SIZE, outlier_frac=DEFAULT_OUTLIER_FRAC, double_quant=False,
-                  dq_group_size=DEFAULT_DQ_GROUP_SIZE, smooth=False, smooth_alpha=DEFAULT_SMOOTH_ALPHA):
+                  dq_group_size=DEFAULT_DQ_GROUP_SIZE, smooth=False, smooth_alpha=DEFAULT_SMOOTH_ALPHA, _topk=None):
     """6-bit RVQ (codec.py:678-737): 4-bit uniform stage 1 (outliers, DQ),
     2-bit uniform residual stage 2 (no outliers, no DQ)."""
     if smooth:
         raise NotImplementedError("smooth=True is not covered by tensorshrink_amd")
     lib = L.lib()
     qt4 = quantize_tensor(w, bits=4, group_size=group_size, outlier_frac=outlier_frac, double_quant=double_quant,
-                          dq_group_size=dq_group_size)
+                          dq_group_size=dq_group_size, _topk=_topk)
     dev = _device()
     w2d, _ = _to_2d(w)
     wg = _gpu_weight(w2d, dev)
@@ -525,19 +614,26 @@ def quantize_tensor_adaptive(
     allowed_bits: Sequence[int] = DEFAULT_ADAPTIVE_BIT_CHAIN,
     companded: bool = False,
     nf_quant: bool = False,
+    _topk=None,
 ) -> Tuple[QuantizedTensor, float, bool]:
-    """Escalating bit-width quantize (codec.py:863-931)."""
+    """Escalating bit-width quantize (codec.py:863-931). The top-k outlier
+    selection depends on the weight and outlier_frac only: it runs once
+    (or comes in as `_topk`, this weight's topk_of()) for the whole chain."""
     if companded and (force_bits == 6 or 6 in allowed_bits):
         raise ValueError("companded=True is not supported with bits=6 (RVQ)")
+    if smooth:
+        raise NotImplementedError("smooth=True is not covered by tensorshrink_amd")
     kw = dict(group_size=group_size, outlier_frac=outlier_frac, double_quant=double_quant,
               dq_group_size=dq_group_size, smooth=smooth, smooth_alpha=smooth_alpha, companded=companded,
-              nf_quant=nf_quant)
+              nf_quant=nf_quant, _topk=_topk)
     if force_bits is not None:
         qt = quantize_tensor(w, bits=force_bits, **kw)
         return qt, relative_error(w, qt), False
     chain = sorted(set(allowed_bits))
     if not chain or any(b not in (2, 4, 6, 8) for b in chain):
         raise ValueError(f"allowed_bits must be a non-empty subset of (2, 4, 6, 8), got {allowed_bits!r}")
+    if _topk is None and len(chain) > 1:
+        kw["_topk"] = topk_of(w, outlier_frac)
     for i, bits in enumerate(chain):
         qt = quantize_tensor(w, bits=bits, **kw)
         err = relative_error(w, qt)

@@ -10,6 +10,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
+#include <deque>
 #include <map>
 #include <mutex>
 #include <set>
@@ -28,12 +29,16 @@ namespace {
 constexpr size_t GEMM_LT_WS = 32u << 20;  // hipBLASLt workspace reserved after W
 constexpr int GEMM_HEURISTIC = 8;          // heuristic candidates, tried first
 constexpr int GEMM_FINALISTS = 4;          // re-timed candidates of the first pass
+constexpr size_t GEMM_CANDIDATES = 16;     // candidates per shape (heuristic's, then others)
+constexpr size_t GEMM_MAX_PLANS = 64;      // exact-shape plans kept (oldest evicted)
+constexpr float GEMM_TUNE_MS = 200.f;      // first-pass timing budget per M bucket
 
 struct Plan {
   hipblasLtMatmulDesc_t desc = nullptr;
   hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
-  std::vector<hipblasLtMatmulAlgo_t> algo;  // heuristic order, then every other supported algorithm
+  std::vector<hipblasLtMatmulAlgo_t> algo;  // heuristic order, then other supported algorithms
   std::vector<size_t> ws;                   // workspace bytes of each
+  std::vector<int> index;                   // the library's stable index of each
   int best = 0;
   bool tuned = false;
   bool ok = false;
@@ -41,10 +46,30 @@ struct Plan {
 
 // (device, M, N, K, ldx, ldy, x dtype, y dtype, bias kind)
 using Key = std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t, int, int, int>;
+// (device, M bucket, N, K, x dtype, y dtype, bias kind): the timing sweep runs
+// once per bucket (M rounded up to a power of two, at least 64) and its
+// winner serves every M of the bucket
+using TuneKey = std::tuple<int, int64_t, int64_t, int64_t, int, int, int>;
 
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
 std::map<Key, Plan> g_plans;
+std::deque<Key> g_plan_order;       // insertion order, for eviction
+std::map<TuneKey, int> g_bucket_best;  // library algorithm index chosen per bucket
+
+int64_t m_bucket(int64_t M) {
+  int64_t b = 64;
+  while (b < M) b <<= 1;
+  return b;
+}
+
+void destroy_plan(Plan& p) {
+  if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
+  if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
+  if (p.d) hipblasLtMatrixLayoutDestroy(p.d);
+  if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+  p = Plan{};
+}
 
 hipDataType hip_type(int dt) { return dt == TS_F32 ? HIP_R_32F : (dt == TS_BF16 ? HIP_R_16BF : HIP_R_16F); }
 
@@ -52,8 +77,11 @@ size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 // y[M, N] (row-major, ld ldy) = x[M, K] (ld ldx) @ W[N, K]^T: in column-major
 // terms D[N, M] = op(A) B with A = W as K x N (transposed), B = x as K x M.
+// Candidates: the heuristic's usable ones, then other supported algorithms up
+// to GEMM_CANDIDATES in all; `keep` (a bucket's earlier winner, or -1) is
+// kept past the cap.
 Plan make_plan(hipblasLtHandle_t h, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, int xdt, int ydt,
-               int bias_kind) {
+               int bias_kind, int keep) {
   Plan p;
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
   if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return p;
@@ -84,9 +112,10 @@ Plan make_plan(hipblasLtHandle_t h, int64_t M, int64_t N, int64_t K, int64_t ldx
     if (heur[i].state == HIPBLAS_STATUS_SUCCESS && heur[i].workspaceSize <= GEMM_LT_WS) {
       p.algo.push_back(heur[i].algo);
       p.ws.push_back(heur[i].workspaceSize);
-      seen.insert(hipblaslt_ext::getIndexFromAlgo(heur[i].algo));
+      p.index.push_back(hipblaslt_ext::getIndexFromAlgo(heur[i].algo));
+      seen.insert(p.index.back());
     }
-  // then every other algorithm of the library that supports this problem
+  // then other algorithms of the library that support this problem
   std::vector<hipblasLtMatmulHeuristicResult_t> all;
   const hipDataType tx = hip_type(xdt), ty = hip_type(ydt);
   if (hipblaslt_ext::getAllAlgos(h, hipblaslt_ext::GemmType::HIPBLASLT_GEMM, HIPBLAS_OP_T, HIPBLAS_OP_N, tx, tx, ty,
@@ -95,6 +124,7 @@ Plan make_plan(hipblasLtHandle_t h, int64_t M, int64_t N, int64_t K, int64_t ldx
     for (auto& r : all) {
       const int idx = hipblaslt_ext::getIndexFromAlgo(r.algo);
       if (idx < 0 || seen.count(idx)) continue;
+      if (p.algo.size() >= GEMM_CANDIDATES && idx != keep) continue;
       size_t wsb = 0;
       if (hipblaslt_ext::matmulIsAlgoSupported(h, p.desc, &alpha, p.a, p.b, &beta, p.d, p.d, r.algo, wsb) !=
               HIPBLAS_STATUS_SUCCESS ||
@@ -103,6 +133,7 @@ Plan make_plan(hipblasLtHandle_t h, int64_t M, int64_t N, int64_t K, int64_t ldx
       seen.insert(idx);
       p.algo.push_back(r.algo);
       p.ws.push_back(wsb);
+      p.index.push_back(idx);
     }
   }
   p.ok = !p.algo.empty();
@@ -137,9 +168,29 @@ int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, 
     hit = g_handles.emplace(dev, h).first;
   }
   const Key key{dev, M, N, K, ldx, ldy, x_dtype, y_dtype, bias ? 1 : 0};
+  const TuneKey tkey{dev, m_bucket(M), N, K, x_dtype, y_dtype, bias ? 1 : 0};
+  const auto bit = g_bucket_best.find(tkey);
+  const int keep = bit != g_bucket_best.end() ? bit->second : -1;
   auto pit = g_plans.find(key);
-  if (pit == g_plans.end()) pit = g_plans.emplace(key, make_plan(hit->second, M, N, K, ldx, ldy, x_dtype, y_dtype,
-                                                                 bias ? 1 : 0)).first;
+  if (pit == g_plans.end()) {
+    while (g_plans.size() >= GEMM_MAX_PLANS && !g_plan_order.empty()) {
+      auto old = g_plans.find(g_plan_order.front());
+      g_plan_order.pop_front();
+      if (old != g_plans.end()) {
+        destroy_plan(old->second);
+        g_plans.erase(old);
+      }
+    }
+    pit = g_plans.emplace(key, make_plan(hit->second, M, N, K, ldx, ldy, x_dtype, y_dtype, bias ? 1 : 0, keep))
+              .first;
+    g_plan_order.push_back(key);
+    Plan& q = pit->second;
+    if (keep >= 0) {  // the bucket was timed before: take its winner if this shape supports it
+      for (size_t i = 0; i < q.index.size(); ++i)
+        if (q.index[i] == keep) q.best = (int)i;
+      q.tuned = true;
+    }
+  }
   Plan& p = pit->second;
   if (!p.ok) return TS_NOT_COVERED;
   if (bias) {
@@ -151,12 +202,13 @@ int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, 
     return hipblasLtMatmul(hit->second, p.desc, &alpha, W, p.a, x, p.b, &beta, y, p.d, y, p.d, &p.algo[i], lt_ws,
                            p.ws[i], st) == HIPBLAS_STATUS_SUCCESS;
   };
-  // The first call of a shape outside graph capture times the candidates on
-  // this call's own operands and keeps the fastest: one warm and one timed
-  // run each, then the best few again over three runs. This is the only call
-  // that waits for the device. Each candidate writes the same y, so the last
-  // one run leaves the right result. Under capture, before tuning, the
-  // heuristic's first choice runs.
+  // The first call of an M bucket outside graph capture times the candidates
+  // on this call's own operands and keeps the fastest: one warm and one timed
+  // run each (stopping once GEMM_TUNE_MS of timed runs have passed), then the
+  // best few again over three runs. This is the only call that waits for the
+  // device; later calls in the bucket, at any M, reuse its winner. Each
+  // candidate writes the same y, so the last one run leaves the right result.
+  // Under capture, before tuning, the heuristic's first choice runs.
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   const int nc = (int)p.algo.size();
   if (!p.tuned && nc > 1 && hipStreamIsCapturing(st, &cap) == hipSuccess && cap == hipStreamCaptureStatusNone) {
@@ -174,10 +226,14 @@ int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, 
         return ms / reps;
       };
       std::vector<std::pair<float, int>> t1;
-      for (int i = 0; i < nc; ++i) t1.emplace_back(time_of(i, 1), i);
+      float spent = 0.f;
+      for (int i = 0; i < nc && spent < GEMM_TUNE_MS; ++i) {
+        t1.emplace_back(time_of(i, 1), i);
+        if (t1.back().first < 1e30f) spent += t1.back().first;
+      }
       std::sort(t1.begin(), t1.end());
       float best_ms = 1e30f;
-      for (int f = 0; f < std::min(nc, GEMM_FINALISTS); ++f) {
+      for (int f = 0; f < std::min((int)t1.size(), GEMM_FINALISTS); ++f) {
         if (t1[f].first >= 1e30f) break;
         const float ms = time_of(t1[f].second, 3);
         if (ms < best_ms) {
@@ -189,6 +245,7 @@ int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, 
     if (e0) hipEventDestroy(e0);
     if (e1) hipEventDestroy(e1);
     p.tuned = true;
+    g_bucket_best[tkey] = p.index[p.best];
   }
   if (!run(p.best)) return TS_HIP_ERROR;
   return TS_OK;

@@ -18,30 +18,35 @@ from .codec import (
     DEFAULT_GROUP_SIZE,
     DEFAULT_OUTLIER_FRAC,
     QuantizedTensor,
+    TopkPrefetch,
     quantize_tensor,
     relative_error,
+    topk_of,
 )
 
 
 def quantize_tensor_gpu(w: torch.Tensor, bits: int = 4, group_size: int = DEFAULT_GROUP_SIZE,
-                        outlier_frac: float = DEFAULT_OUTLIER_FRAC) -> QuantizedTensor:
+                        outlier_frac: float = DEFAULT_OUTLIER_FRAC, _topk=None) -> QuantizedTensor:
     if bits not in (2, 4, 8):
         raise ValueError("bits must be 2, 4, or 8")
     if w.dim() == 1:
         raise ValueError("quantize_tensor_gpu expects ndim >= 2")
-    return quantize_tensor(w, bits=bits, group_size=group_size, outlier_frac=outlier_frac)
+    return quantize_tensor(w, bits=bits, group_size=group_size, outlier_frac=outlier_frac, _topk=_topk)
 
 
 def quantize_tensor_gpu_adaptive(w: torch.Tensor, group_size: int = DEFAULT_GROUP_SIZE,
                                  outlier_frac: float = DEFAULT_OUTLIER_FRAC,
                                  error_threshold: float = DEFAULT_ERROR_THRESHOLD,
-                                 force_bits: Optional[int] = None) -> Tuple[QuantizedTensor, float, bool]:
-    """2 -> 4 -> 8 escalation (gpu_quantize.py:169-209)."""
+                                 force_bits: Optional[int] = None, _topk=None) -> Tuple[QuantizedTensor, float, bool]:
+    """2 -> 4 -> 8 escalation (gpu_quantize.py:169-209), the top-k outlier
+    selection computed once for the chain."""
     if force_bits is not None:
-        qt = quantize_tensor_gpu(w, bits=force_bits, group_size=group_size, outlier_frac=outlier_frac)
+        qt = quantize_tensor_gpu(w, bits=force_bits, group_size=group_size, outlier_frac=outlier_frac, _topk=_topk)
         return qt, relative_error(w, qt), False
+    if _topk is None:
+        _topk = topk_of(w, outlier_frac)
     for i, bits in enumerate((2, 4, 8)):
-        qt = quantize_tensor_gpu(w, bits=bits, group_size=group_size, outlier_frac=outlier_frac)
+        qt = quantize_tensor_gpu(w, bits=bits, group_size=group_size, outlier_frac=outlier_frac, _topk=_topk)
         err = relative_error(w, qt)
         if err <= error_threshold or bits == 8:
             return qt, err, i > 0
@@ -66,26 +71,31 @@ def quantize_module_gpu(model: torch.nn.Module, device: str = "cuda", bits: int 
     stats = {"n_replaced": 0, "orig_bytes": 0, "packed_bytes": 0, "layers": [], "cache": None}
     dev = torch.device(device)
     plan = {}
+    workers = int(quantize_workers or 4)
     if vram_budget_mb is not None:
         ls = []
-        for name, lin in targets:
+        pre = TopkPrefetch([lin.weight.data for _, lin in targets], outlier_frac, workers)
+        for i, (name, lin) in enumerate(targets):
             wg = lin.weight.data.to(dev)
-            q4 = quantize_tensor_gpu(wg, 4, group_size, outlier_frac)
-            q8 = quantize_tensor_gpu(wg, 8, group_size, outlier_frac)
+            tk = pre.get(i)
+            q4 = quantize_tensor_gpu(wg, 4, group_size, outlier_frac, _topk=tk)
+            q8 = quantize_tensor_gpu(wg, 8, group_size, outlier_frac, _topk=tk)
             ls.append(LayerBitStats(name, estimate_resident_nbytes(q4), estimate_resident_nbytes(q8),
                                     relative_error(lin.weight.data, q4), relative_error(lin.weight.data, q8)))
         plan = budget_allocate_bits(ls, vram_budget_mb * 1024 * 1024)
-    for name, lin in targets:
+    pre = TopkPrefetch([lin.weight.data for _, lin in targets], outlier_frac, workers)
+    for i, (name, lin) in enumerate(targets):
         w = lin.weight.data
         wg = w.to(dev)
         f32 = any(p in name.lower() for p in fp32_pats)
+        tk = pre.get(i)
         if vram_budget_mb is not None:
-            qt = quantize_tensor_gpu(wg, plan[name], group_size, outlier_frac)
+            qt = quantize_tensor_gpu(wg, plan[name], group_size, outlier_frac, _topk=tk)
             err, esc = relative_error(w, qt), plan[name] == 8
         elif adaptive:
-            qt, err, esc = quantize_tensor_gpu_adaptive(wg, group_size, outlier_frac, error_threshold)
+            qt, err, esc = quantize_tensor_gpu_adaptive(wg, group_size, outlier_frac, error_threshold, _topk=tk)
         else:
-            qt = quantize_tensor_gpu(wg, bits, group_size, outlier_frac)
+            qt = quantize_tensor_gpu(wg, bits, group_size, outlier_frac, _topk=tk)
             err, esc = relative_error(w, qt), False
         bias = lin.bias.data if lin.bias is not None else None
         qlin = QuantLinear(qt, bias, max_dequant_rows=max_dequant_rows, force_fp32_compute=f32,

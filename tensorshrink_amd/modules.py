@@ -42,6 +42,7 @@ from .codec import (
     DEFAULT_DQ_GROUP_SIZE,
     LayerBitStats,
     QuantizedTensor,
+    TopkPrefetch,
     budget_allocate_bits,
     estimate_resident_nbytes as _estimate_resident_nbytes,
     quantize_tensor,
@@ -412,17 +413,19 @@ class QuantLinear(nn.Module):
                     max_dequant_rows: Union[int, str] = DEFAULT_MAX_DEQUANT_ROWS, force_fp32_compute: bool = False,
                     cache=None, fast_dequant: bool = True, use_triton: bool = True, companded: bool = False,
                     double_quant: bool = True, dq_group_size: int = DEFAULT_DQ_GROUP_SIZE,
-                    nf_quant: bool = True) -> Tuple["QuantLinear", float, bool]:
-        """modules.py:942-1003."""
+                    nf_quant: bool = True, _topk=None) -> Tuple["QuantLinear", float, bool]:
+        """modules.py:942-1003. (`_topk`, not part of the reference's
+        signature: the weight's codec.topk_of() result, computed ahead.)"""
         w = linear.weight.data
         if adaptive:
             qt, err, escalated = quantize_tensor_adaptive(
                 w, group_size=group_size, outlier_frac=outlier_frac, error_threshold=error_threshold,
                 allowed_bits=(2, 4, 8), companded=companded, double_quant=double_quant,
-                dq_group_size=dq_group_size, nf_quant=nf_quant)
+                dq_group_size=dq_group_size, nf_quant=nf_quant, _topk=_topk)
         else:
             qt = quantize_tensor(w, bits=bits, group_size=group_size, outlier_frac=outlier_frac, companded=companded,
-                                 double_quant=double_quant, dq_group_size=dq_group_size, nf_quant=nf_quant)
+                                 double_quant=double_quant, dq_group_size=dq_group_size, nf_quant=nf_quant,
+                                 _topk=_topk)
             err = relative_error(w, qt)
             escalated = False
         bias = linear.bias.data if linear.bias is not None else None
@@ -497,8 +500,11 @@ def quantize_module(
     nf_quant: bool = True,
 ) -> dict:
     """Replace every eligible nn.Linear with a QuantLinear, in place
-    (modules.py:1258-1455). Layers are quantized on the GPU one after another;
-    `quantize_workers` is accepted for signature compatibility."""
+    (modules.py:1258-1455). Layers are quantized on the GPU one after another,
+    in order; the host side of each layer's top-k outlier selection (a
+    sequential heap replay that fixes torch.topk's order) runs ahead of the
+    loop on `quantize_workers` threads, one layer per thread, and is shared by
+    every bit width a layer is quantized at."""
     if cache_budget_mb > 0 or host_cache_budget_mb > 0:
         raise NotImplementedError("WeightCache is not part of the tensorshrink_amd path")
     targets = list(_iter_target_linears(model, min_numel, skip_name_patterns))
@@ -521,10 +527,12 @@ def quantize_module(
         if companded:
             raise ValueError("companded=True is not yet supported with vram_budget_mb (budget-aware path)")
         computed, lstats = {}, []
-        for name, lin in targets:
+        pre = TopkPrefetch([lin.weight.data for _, lin in targets], outlier_frac, int(quantize_workers or 1))
+        for i, (name, lin) in enumerate(targets):
             w = lin.weight.data
-            q4 = quantize_tensor(w, bits=4, group_size=group_size, outlier_frac=outlier_frac)
-            q8 = quantize_tensor(w, bits=8, group_size=group_size, outlier_frac=outlier_frac)
+            tk = pre.get(i)
+            q4 = quantize_tensor(w, bits=4, group_size=group_size, outlier_frac=outlier_frac, _topk=tk)
+            q8 = quantize_tensor(w, bits=8, group_size=group_size, outlier_frac=outlier_frac, _topk=tk)
             e4, e8 = relative_error(w, q4), relative_error(w, q8)
             lstats.append(LayerBitStats(name, _estimate_resident_nbytes(q4), _estimate_resident_nbytes(q8), e4, e8))
             computed[name] = {4: (q4, e4), 8: (q8, e8)}
@@ -542,13 +550,14 @@ def quantize_module(
         stats["budget_bytes_used"] = stats["packed_bytes"]
         return stats
 
+    pre = TopkPrefetch([lin.weight.data for _, lin in targets], outlier_frac, int(quantize_workers or 1))
     for i, (name, lin) in enumerate(targets):
         f32 = any(p in name.lower() for p in fp32_pats)
         qlin, err, esc = QuantLinear.from_linear(
             lin, bits=bits, group_size=group_size, outlier_frac=outlier_frac, adaptive=adaptive,
             error_threshold=error_threshold, max_dequant_rows=max_dequant_rows, force_fp32_compute=f32,
             fast_dequant=fast_dequant, use_triton=use_triton, companded=companded, double_quant=double_quant,
-            dq_group_size=dq_group_size, nf_quant=nf_quant)
+            dq_group_size=dq_group_size, nf_quant=nf_quant, _topk=pre.get(i))
         _set_module_by_name(model, name, qlin)
         targets[i] = None
         record(name, qlin, err, esc, f32, lin.weight.element_size())

@@ -142,3 +142,18 @@ def test_quantize_nan_weights_matches_reference(case):
         assert str(v.dtype) == exp["dtype"] and list(v.shape) == exp["shape"], f
         bits = v.view(np.uint16) if v.dtype == np.float16 else v
         np.testing.assert_array_equal(bits.reshape(-1), np.asarray(exp["values"], dtype=bits.dtype), err_msg=f)
+
+
+@pytest.mark.parametrize("adaptive", [False, True])
+def test_quantize_module_workers_identical(adaptive):
+    """The top-k replays computed ahead on a thread pool (quantize_workers)
+    give the same layers, bit for bit, as computing them inline."""
+    import tensorshrink_amd as ts
+    dig = []
+    for workers in (1, 4):
+        model = recipes.tiny_model()
+        stats = ts.quantize_module(model, verbose=False, quantize_workers=workers, adaptive=adaptive,
+                                   error_threshold=0.09)
+        dig.append(({n: _digests(m) for n, m in model.named_modules() if isinstance(m, ts.QuantLinear)},
+                    [(l["name"], l["bits"], l["escalated"]) for l in stats["layers"]]))
+    assert dig[0] == dig[1]

@@ -454,3 +454,20 @@ def test_forward_group_persistent_schedule():
             say("persistent group", M, err)
             assert err <= TOL, (M, err)
             assert max_rel_err(y.float(), q(x).float()) <= 1e-3
+
+
+def test_gemm_path_m_buckets():
+    """The dequantize + library GEMM path (a workspace passed through the
+    C-ABI) over many prompt lengths: one timing sweep per power-of-two M
+    bucket, its winner reused at every M of the bucket, and more distinct
+    shapes than the plan cache keeps (the oldest are evicted), each result
+    against x @ W^T."""
+    ql, W = _layer(512, 1024, 93, NF4)
+    Ms = list(range(65, 140)) + [200, 256, 257, 1000]
+    for M in Ms:
+        x = recipes.activations(M, 1024, seed=M).cuda()
+        err = max_rel_err(_forward_gemm(ql, x).float(), x.float() @ W.T)
+        assert err <= TOL, (M, err)
+    # a shape evicted earlier is planned again and still right
+    x = recipes.activations(65, 1024, seed=65).cuda()
+    assert max_rel_err(_forward_gemm(ql, x).float(), x.float() @ W.T) <= TOL
