@@ -300,9 +300,22 @@ class QuantLinear(nn.Module):
         row = self.outlier_row.cpu().numpy().astype(np.int64)
         col = self.outlier_col.cpu().numpy().astype(np.int64)
         idx = (row * self.cols + col).astype(np.int32)
-        w = self.dequantize_weight(torch.float32)
-        oval = w.reshape(-1)[torch.from_numpy(idx.astype(np.int64)).to(w.device)].to(torch.float16).cpu().numpy() \
-            if idx.size else np.zeros(0, np.float16)
+        if self.bits == 6:
+            # RVQ: the delta is relative to stage 1 (the stage-2 residual is
+            # added everywhere, outliers included), so the stored value is
+            # f16(stage-1 base + delta)
+            s1 = self._make_layer(with_outliers=False)
+            s1.bits, s1.stage2_packed, s1.stage2_scale, s1.stage2_gmin, s1.stage2_stride = 4, None, None, None, 0
+            base = torch.empty(self.rows, self.cols, dtype=torch.float32, device=self.packed.device)
+            L.check(L.lib().ts_dequantize(ctypes.byref(s1), L.TS_DEQ_QLINEAR, None, None, 0, base.data_ptr(),
+                                          self.cols, L.dtype_code(torch.float32), L.stream_ptr(self.packed.device)),
+                    "dequantize")
+            w = base.reshape(-1)[torch.from_numpy(idx.astype(np.int64)).to(base.device)] + \
+                self.outlier_delta.to(torch.float32)
+        else:
+            w = self.dequantize_weight(torch.float32).reshape(-1)[
+                torch.from_numpy(idx.astype(np.int64)).to(self.packed.device)]
+        oval = w.to(torch.float16).cpu().numpy() if idx.size else np.zeros(0, np.float16)
         kw = dict(orig_shape=(self.out_features, self.in_features), orig_dtype=self.orig_dtype_str, bits=self.bits,
                   group_size=self.group_size, rows=self.rows, cols=self.cols, padded_cols=self.padded_cols,
                   n_groups=self.n_groups, packed=self.packed.cpu().numpy(), outlier_idx=idx, outlier_val=oval)

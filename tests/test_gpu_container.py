@@ -150,3 +150,41 @@ def test_stream_quantize_budget_plan(tmp_path):
             qt = ts.quantize_tensor(sd[name], bits=bits, group_size=128, outlier_frac=0.003)
             _same_qt(r.get_quantized(name), qt)
             assert r.manifest["tensors"][name]["escalated"] == (bits == 8)
+
+
+@pytest.mark.parametrize("opts", [dict(bits=6, group_size=64, outlier_frac=0.002),
+                                  dict(bits=2, group_size=64, outlier_frac=0.001, companded=True),
+                                  dict(bits=8, group_size=128, outlier_frac=0.0, double_quant=True, nf_quant=True)])
+def test_save_load_formats(tmp_path, opts):
+    """6-bit RVQ (stage-2 parts stored), companded 2-bit (codebook part) and a
+    layer without outliers through save_quant_module -> load_quantized_module:
+    the reloaded layer's weights and forward equal the original's."""
+    import tensorshrink_amd as ts
+    w = recipes.student_t_weight(384, 512, 61)
+    lin = torch.nn.Linear(512, 384, bias=True, dtype=torch.float16)
+    lin.weight.data = w.half()
+    lin.bias.data = (torch.randn(384, generator=torch.Generator().manual_seed(2)) * 0.1).half()
+    model = torch.nn.Sequential(lin)
+    qt = ts.quantize_tensor(lin.weight.data, **opts)
+    model[0] = ts.QuantLinear(qt, lin.bias.data)
+    ts.save_quant_module(model, tmp_path / "f.tsk", verbose=False)
+    fresh = torch.nn.Sequential(torch.nn.Linear(512, 384, bias=True, dtype=torch.float16))
+    with ts.ContainerReader(tmp_path / "f.tsk") as r:
+        ts.load_quantized_module(fresh, r, verbose=False)
+        e = r.manifest["tensors"]["0.weight"]
+        # any codebook part (NF or Lloyd-Max) marks the entry "companded" (container.py:203-206)
+        has_cb = bool(opts.get("companded") or opts.get("nf_quant"))
+        assert e["bits"] == opts["bits"] and e.get("companded", False) == has_cb
+        if opts["bits"] == 6:
+            assert "stage2_packed" in e["segments_v2"]["parts"]
+    q0, q1 = model[0], fresh[0]
+    assert isinstance(q1, ts.QuantLinear) and q1.bits == q0.bits
+    w0, w1 = q0.dequantize_weight(torch.float32), q1.dequantize_weight(torch.float32)
+    assert float((w0 - w1).abs().max()) <= 1e-3 * float(w0.abs().max())
+    # a double-quant layer reloads with the f16 scale/gmin (no DQ codes in the
+    # container): outputs within a bf16 ulp or two
+    tol = 1e-2 if opts.get("double_quant") else 1e-3
+    for M in (1, 20):
+        x = recipes.activations(M, 512, seed=M).cuda()
+        y0, y1 = q0(x).float(), q1(x).float()
+        assert float((y0 - y1).abs().max()) <= tol * float(y0.abs().max()), M

@@ -205,3 +205,20 @@ def test_reassigned_tensors_rebuild_the_view():
     assert ql.outlier_row_ptr.dtype == torch.int32 and ql.tile_outliers.dtype == torch.int64
     for x, r in zip(xs, ref):
         assert torch.equal(ql(x), r)
+
+
+def test_streaming_and_graphs_bf16_model():
+    """A model cast to bf16 (QuantLinear keeps its metadata dtypes) streamed
+    from host memory, then captured: outputs equal the resident model's."""
+    import tensorshrink_amd as ts
+    model = _stack(4).to(torch.bfloat16)
+    x = recipes.activations(3, K, seed=9).cuda()
+    with torch.no_grad():
+        ref = model(x)
+        st = ts.stream_offload_module(model, verbose=False)
+        assert torch.equal(model(x), ref)
+        st.disable()
+        model.cuda()
+        g = ts.CUDAGraphQuantModel(model)
+        for _ in range(3):
+            assert torch.equal(g(x), ref)
