@@ -16,6 +16,10 @@ typedef float ts_f32x4 __attribute__((ext_vector_type(4)));
 typedef float ts_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t ts_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t ts_u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 ts_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 ts_f16x2 __attribute__((ext_vector_type(2)));
+typedef float ts_f32x2 __attribute__((ext_vector_type(2)));
+typedef short ts_s16x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // scalar conversions (IEEE, round to nearest even, subnormals kept)

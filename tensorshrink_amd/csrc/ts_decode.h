@@ -141,6 +141,23 @@ TS_DEV Bytes<NB> load_bytes(const uint8_t* p) {
   return b;
 }
 
+// v moved within a 16-lane row by DPP control CTRL (every source lane valid).
+template <int CTRL>
+TS_DEV float ts_dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// v[l] + v[l ^ 32] and v[l] + v[l ^ 16] on every lane.
+TS_DEV float ts_sum_x32(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const auto p = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+}
+TS_DEV float ts_sum_x16(float v) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, v);
+  const auto p = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+  return __builtin_bit_cast(float, (uint32_t)p[0]) + __builtin_bit_cast(float, (uint32_t)p[1]);
+}
+
 TS_DEV uint32_t byte_of(const uint32_t* d, int i) { return (d[i >> 2] >> (8 * (i & 3))) & 0xffu; }
 TS_DEV uint32_t half_of(const uint32_t* d, int i) { return (d[i >> 1] >> (16 * (i & 1))) & 0xffffu; }
 
@@ -415,6 +432,30 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       if constexpr (CPM == 8) *reinterpret_cast<ts_u32x4*>(xw + lane * 8) = B.xv;
       else *reinterpret_cast<ts_u32x2*>(xw + lane * 4) = ts_u32x2{B.xv.x, B.xv.y};
     }
+    // M = 1: the gmin term's x . 1 sums, one per group and the same for every
+    // row, from the chunks the lanes already hold instead of one MFMA per
+    // chunk against ones: each lane sums its chunk (dot2 with ones, fp32),
+    // DPP sums the NMF lanes of a (group, lane quarter) segment and two
+    // permlane swaps sum the four quarters, so lane u * NMF ends with group
+    // u's total.
+    float xsum = 0.f;
+    if constexpr (XM == XM_SLOT) {
+      auto dot1 = [&](uint32_t v, float c) {
+        if constexpr (BF16)
+          return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ts_bf16x2, v),
+                                                 __builtin_bit_cast(ts_bf16x2, 0x3f803f80u), c, false);
+        else
+          return __builtin_amdgcn_fdot2(__builtin_bit_cast(ts_f16x2, v), __builtin_bit_cast(ts_f16x2, 0x3c003c00u), c,
+                                        false);
+      };
+      xsum = dot1(B.xv.y, dot1(B.xv.x, 0.f));
+      if constexpr (CPM == 8) xsum = dot1(B.xv.w, dot1(B.xv.z, xsum));
+      if constexpr (NMF >= 2) xsum += ts_dpp_f<0xB1>(xsum);   // quad_perm [1,0,3,2]
+      if constexpr (NMF >= 4) xsum += ts_dpp_f<0x4E>(xsum);   // quad_perm [2,3,0,1]
+      if constexpr (NMF >= 8) xsum += ts_dpp_f<0x141>(xsum);  // row_half_mirror
+      if constexpr (NMF >= 16) xsum += ts_dpp_f<0x140>(xsum); // row_mirror
+      xsum = ts_sum_x16(ts_sum_x32(xsum));
+    }
     // the batch's code dwords per group (TQ: after the quarter transpose)
     uint32_t wt[TQ ? U : 1];
     if constexpr (TQ) {
@@ -509,9 +550,11 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
 #pragma unroll
       for (int j = 0; j < NMF; ++j) {
         aw = ts_mfma16x16x32<BF16>(xa[j], bv[j], aw);
-        ax = ts_mfma16x16x32<BF16>(xa[j], ones, ax);
+        if constexpr (XM != XM_SLOT) ax = ts_mfma16x16x32<BF16>(xa[j], ones, ax);
         if constexpr (RVQ) aw2 = ts_mfma16x16x32<BF16>(xa[j], bv2[j], aw2);
       }
+      if constexpr (XM == XM_SLOT)
+        ax[0] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, xsum), u * NMF));
       float s2_ = 0.f, g2_ = 0.f;
       if constexpr (RVQ) {
         s2_ = ts_h2f((uint16_t)(AL ? half_of(B.s2s, u) : B.s2s[u]));

@@ -91,11 +91,6 @@ constexpr uint32_t PF_NO_COL = 0xffffu;  // column of the "no more outliers" ent
 #define PF_NW_WIDE 8  // waves per workgroup of the 256 x 256 tile
 #endif
 
-typedef __bf16 ts_bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 ts_f16x2 __attribute__((ext_vector_type(2)));
-typedef float ts_f32x2 __attribute__((ext_vector_type(2)));
-typedef short ts_s16x2 __attribute__((ext_vector_type(2)));
-
 // Two floats -> packed (lo, hi) bf16/f16 pair, round to nearest even
 // (v_cvt_pk_bf16_f32 on gfx950).
 template <bool BF16>
