@@ -20,8 +20,10 @@
 //     bank-private copies (up to one per lane of a half-wave).
 //   * The per-group affine is factorised out of the MFMA:
 //         y += s[n,g] * (x . cb[c]) + gmin[n,g] * (x . 1)
-//     with both dot products on the matrix core and s/gmin in float32
-//     (rebuilt from double-quant codes in-register, modules.py:573-579).
+//     with s/gmin in float32 (rebuilt from double-quant codes in-register,
+//     modules.py:573-579). x . cb[c] runs on the matrix core; x . 1 too at
+//     M > 1, while at M = 1 (one sum per group, the same for every row) it is
+//     a lane reduction of the x chunks the lanes already hold.
 //   * x at M = 1 comes in one 16-byte load per lane and batch, is written to
 //     a wave-private LDS slot and read back per MFMA with the 16 lanes of a
 //     row on one address (a broadcast read, no VALU); at M > 1 it is
