@@ -73,7 +73,9 @@ typedef struct {
    * CSR tables by ts_build_tile_outliers; no counterpart in the reference):
    * tile t owns slots [t * tile_outlier_cap, (t + 1) * tile_outlier_cap), each
    * u64 = col | (row - 16 t) << 32 | f16 delta bits << 48; unused slots are 0.
-   * NULL / 0 when the layer has no outliers. */
+   * NULL / 0 when the layer has no outliers, or to make the decode kernel read
+   * the outliers through outlier_row_ptr instead (outliers crowded into a few
+   * tiles, where every tile padded to the fullest one would be too large). */
   const uint64_t* tile_outliers;
   int64_t tile_outlier_cap;
   /* Optional host copy of `codebook` (no counterpart in the reference). With

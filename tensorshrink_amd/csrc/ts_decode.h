@@ -71,7 +71,7 @@ struct DecodeArgs {
   const uint16_t* s2gmin;
   const uint64_t* slots;     // per-tile outlier slots (ts_qlayer.tile_outliers), or any valid
                              // 8-byte array when cap == 0
-  int32_t cap;               // slots per tile (0: no outliers)
+  int32_t cap;               // slots per tile (0: no outliers; -1: DecodeCsr instead)
   const uint16_t* x;
   int64_t ldx;
   void* y;
@@ -96,10 +96,21 @@ struct DecodeArgs {
 // takes the arguments of the layer its tile belongs to.
 constexpr int DEC_GMAX = 4;  // layers per launch
 enum { CB_UNIFORM = 0, CB_INLINE = 1, CB_DEVICE = 2 };
+// A layer without the slot table (outliers crowded into a few tiles, so the
+// padded table was not built; cap == -1): each tile reads its outliers from
+// the row-sorted tables through the CSR row offsets. Kept apart from
+// DecodeArgs, which every workgroup copies into SGPRs at entry.
+struct DecodeCsr {
+  const int32_t* row_ptr;
+  const int32_t* row;
+  const int32_t* col;
+  const uint16_t* delta;
+};
 struct DecodeGroup {
   DecodeArgs a[DEC_GMAX];
   int64_t tile_end[DEC_GMAX];  // cumulative tile counts
   int n;
+  DecodeCsr csr[DEC_GMAX];
 };
 
 constexpr size_t DEC_XLDS_MAX = 64 * 1024;  // activations staged in LDS up to this size
@@ -772,10 +783,27 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   }
   ts_lds_barrier();
 
+  // The tile's outliers through the CSR row offsets (csr layers), added into
+  // the wave's partials rw like the slots: the tile's rows own one
+  // contiguous range of the row-sorted tables.
+  auto add_csr = [&](const DecodeArgs& A, int64_t t, float* rw) {
+    const DecodeCsr& C = g.csr[li];
+    const int64_t r_lo = t * 16;
+    const int32_t b = C.row_ptr[min(r_lo, A.N)], e = C.row_ptr[min(r_lo + 16, A.N)];
+    for (int32_t i = b + tid; i < e; i += NT) {
+      const uint32_t row = (uint32_t)(C.row[i] - r_lo), col = (uint32_t)C.col[i];
+      const float d = ts_h2f(C.delta[i]);
+      for (int m = 0; m < A.M; ++m) {
+        const float xv = XLDS ? XT<BF16>::to_f(xs[m * A.K + col]) : XT<BF16>::to_f(A.x[(int64_t)m * A.ldx + col]);
+        atomicAdd(&rw[(row + 16 * (m >> 2)) * 4 + (m & 3)], xv * d);
+      }
+    }
+  };
+
   if constexpr (RT == 2) {
     static_assert(NB == 1 && XM == XM_GLOBAL && BITS == 4 && !RVQ && !TQ, "two row tiles: 4-bit, x from global");
     const int capm1 = max(a.cap - 1, 0);
-    auto load_slot = [&](int64_t t, int i) { return a.slots[t * a.cap + min(i, capm1)]; };
+    auto load_slot = [&](int64_t t, int i) { return a.slots[t * max(a.cap, 0) + min(i, capm1)]; };
     auto load_bias = [&](int64_t t) { return a.bias_src[min(t * 16 + ((tid >> 2) & 15), a.N - 1) * a.bias_mul]; };
     // reduce the waves' partials of tile t (buffers of parity par), outliers,
     // bias, store; the same steps as the single-tile epilogue below
@@ -794,6 +822,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
         };
         if (tid < a.cap) add_slot(slot0);
         for (int i = tid + NT; i < a.cap; i += NT) add_slot(a.slots[t * a.cap + i]);
+      } else if (a.cap < 0) {
+        add_csr(a, t, rd + wave * 64 * 4);
       }
       ts_lds_barrier();
       if (tid < 256) {
@@ -855,6 +885,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       };
       if (tid < A.cap) add_slot(slot0);
       for (int i = tid + NT; i < A.cap; i += NT) add_slot(A.slots[t * A.cap + i]);  // rare: > NT in a tile
+    } else if (A.cap < 0) {
+      add_csr(A, t, rb + wave * 64 * 4);
     }
     ts_lds_barrier();
     // the tile's 16 x 16 (token m, row nn) outputs: the thread that sums one
@@ -887,7 +919,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // This tile's outlier slots sit at a fixed address (no dependent load):
   // each thread takes slot tid; more (rare: over NT in a tile) are read in
   // the epilogue. Indices past cap read a valid slot whose value is dropped.
-  const int64_t sbase = tile * a.cap;
+  const int64_t sbase = tile * max(a.cap, 0);
   const int capm1 = max(a.cap - 1, 0);
   const uint64_t slot0 = a.slots[sbase + min(tid, capm1)];
   // bias of the output this thread stores (16 rows x M; entry 0 of a valid

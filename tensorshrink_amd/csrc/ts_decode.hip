@@ -4,10 +4,10 @@
 
 namespace ts {
 
-// Kernel arguments of one layer; NOT_COVERED when it has outliers but no
-// per-tile outlier slots.
+// Kernel arguments of one layer; NOT_COVERED when it has outliers but
+// neither per-tile outlier slots nor the CSR row offsets.
 static int fill_args(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, void* y, int64_t ldy,
-                     int y_dtype, const uint16_t* bias, DecodeArgs& a) {
+                     int y_dtype, const uint16_t* bias, DecodeArgs& a, DecodeCsr& c) {
   a = DecodeArgs{};
   a.packed = L->packed;
   a.pstride = L->packed_stride;
@@ -26,11 +26,17 @@ static int fill_args(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t l
   // The kernel's table loads are unconditional. With no outliers (or no
   // codebook, or no bias) they read entry 0 of the packed buffer (at least 16
   // bytes), and the values are never used.
-  if (L->n_outliers > 0 && !L->tile_outliers) return TS_NOT_COVERED;  // needs the per-tile slots
   const void* dummy = L->packed;
   const bool has_out = L->n_outliers > 0;
-  a.slots = has_out ? L->tile_outliers : static_cast<const uint64_t*>(dummy);
-  a.cap = has_out ? (int32_t)L->tile_outlier_cap : 0;
+  const bool slots = has_out && L->tile_outliers && L->tile_outlier_cap > 0;
+  const bool csr = has_out && !slots && L->outlier_row_ptr && L->outlier_row && L->outlier_col && L->outlier_delta;
+  if (has_out && !slots && !csr) return TS_NOT_COVERED;
+  a.slots = slots ? L->tile_outliers : static_cast<const uint64_t*>(dummy);
+  a.cap = slots ? (int32_t)L->tile_outlier_cap : (csr ? -1 : 0);
+  c.row_ptr = csr ? L->outlier_row_ptr : static_cast<const int32_t*>(dummy);
+  c.row = csr ? L->outlier_row : static_cast<const int32_t*>(dummy);
+  c.col = csr ? L->outlier_col : static_cast<const int32_t*>(dummy);
+  c.delta = csr ? L->outlier_delta : static_cast<const uint16_t*>(dummy);
   a.cbsrc = L->codebook ? L->codebook : static_cast<const float*>(dummy);
   const int ncb = 1 << (L->bits == 6 ? 4 : L->bits);
   a.cb_mode = !L->codebook ? CB_UNIFORM : (L->codebook_host && ncb <= 16) ? CB_INLINE : CB_DEVICE;
@@ -74,7 +80,7 @@ static int dispatch(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t s
 int decode_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
                    int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st) {
   DecodeGroup g{};
-  const int rc = fill_args(L, x, M, ldx, y, ldy, y_dtype, bias, g.a[0]);
+  const int rc = fill_args(L, x, M, ldx, y, ldy, y_dtype, bias, g.a[0], g.csr[0]);
   if (rc != TS_OK) return rc;
   g.tile_end[0] = g.a[0].n_tiles;
   g.n = 1;
@@ -99,7 +105,8 @@ int decode_forward_group(const ts_qlayer* const* layers, int n, const uint16_t* 
   int64_t tiles = 0;
   for (int l = 0; l < n; ++l) {
     if (!same_format(layers[0], layers[l])) return TS_NOT_COVERED;
-    const int rc = fill_args(layers[l], x, M, ldx, y[l], ldy[l], y_dtype, bias ? bias[l] : nullptr, g.a[l]);
+    const int rc =
+        fill_args(layers[l], x, M, ldx, y[l], ldy[l], y_dtype, bias ? bias[l] : nullptr, g.a[l], g.csr[l]);
     if (rc != TS_OK) return rc;
     tiles += g.a[l].n_tiles;
     g.tile_end[l] = tiles;

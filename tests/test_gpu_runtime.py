@@ -157,8 +157,9 @@ def test_streaming_matches_resident(depth):
 
 def test_slot_table_bound():
     """Outliers crowded into one 16-row tile of a 16384-row layer would pad
-    every tile to about 4000 slots; the table is not built and M <= 16 takes the
-    generic kernel, with the same result."""
+    every tile to about 4000 slots; the table is not built and the decode
+    kernel (M <= 16) reads each tile's outliers through the CSR row offsets,
+    with the same result."""
     import tensorshrink_amd as ts
     from oracle import codec_ref as O
     w = recipes.gaussian_weight(16384, 256, 91, outlier_frac=0.0)
@@ -176,6 +177,70 @@ def test_slot_table_bound():
         err = float((ql(x).float() - ref).abs().max() / ref.abs().max())
         say("slot bound", M, err)
         assert err <= 1e-2, (M, err)
+
+
+def _csr_view(q):
+    """A copy of the layer's kernel view without the per-tile slot table."""
+    from tensorshrink_amd import _lib as L
+    v = L.QLayer.from_buffer_copy(q._layer)
+    v.tile_outliers = None
+    v.tile_outlier_cap = 0
+    return v
+
+
+@pytest.mark.parametrize("fmt", [dict(bits=4, double_quant=True, nf_quant=True), dict(bits=8, nf_quant=True),
+                                 dict(bits=2, companded=True, group_size=64)])
+def test_decode_csr_outliers_match_slots(fmt):
+    """Without the per-tile slot table the decode kernel reads each tile's
+    outliers through the CSR row offsets: the same outputs as with the slots,
+    in one launch per layer (x through the wave slots at M = 1, staged in LDS
+    at M = 4 / 16) and in a grouped launch, which reports "not covered"
+    (status 1) unless the decode kernel takes every layer."""
+    import ctypes
+    import tensorshrink_amd as ts
+    from tensorshrink_amd import _lib as L
+    qls = [ts.QuantLinear(ts.quantize_tensor(recipes.gaussian_weight(n, K, 60 + i), outlier_frac=0.01, **fmt))
+           for i, n in enumerate((300, 200))]
+    views = [_csr_view(q) for q in qls]
+    lib = L.load()
+    for M in (1, 4, 16):
+        x = recipes.activations(M, K, seed=M).cuda()
+        dt = L.dtype_code(x.dtype)
+        refs = [q(x) for q in qls]  # slot table
+        ys = []
+        for q, v, r in zip(qls, views, refs):
+            y = torch.empty(M, q.out_features, dtype=x.dtype, device="cuda")
+            rc = lib.ts_qlinear_forward(ctypes.byref(v), x.data_ptr(), M, K, dt, y.data_ptr(), q.out_features, dt,
+                                        None, None, 0, L.stream_ptr())
+            assert rc == L.TS_OK
+            ys.append(y)
+        yg = [torch.empty(M, q.out_features, dtype=x.dtype, device="cuda") for q in qls]
+        rc = lib.ts_qlinear_forward_group((ctypes.POINTER(L.QLayer) * 2)(*[ctypes.pointer(v) for v in views]), 2,
+                                          x.data_ptr(), M, K, dt, (ctypes.c_void_p * 2)(*[y.data_ptr() for y in yg]),
+                                          (ctypes.c_int64 * 2)(*[q.out_features for q in qls]), dt,
+                                          (ctypes.c_void_p * 2)(None, None), L.stream_ptr())
+        assert rc == L.TS_OK, rc
+        for r, y, g in zip(refs, ys, yg):
+            scale = r.float().abs().max()
+            assert float((y.float() - r.float()).abs().max() / scale) <= 2e-3
+            assert float((g.float() - r.float()).abs().max() / scale) <= 2e-3
+
+
+def test_decode_csr_outliers_two_tiles_per_workgroup():
+    """The CSR outliers in the two-tile workgroups of large M = 16 launches
+    (4-bit, x read from L2)."""
+    import ctypes
+    import tensorshrink_amd as ts
+    from tensorshrink_amd import _lib as L
+    q = ts.QuantLinear(ts.quantize_tensor(recipes.gaussian_weight(8192, 4096, 66), bits=4, outlier_frac=0.002))
+    v = _csr_view(q)
+    x = recipes.activations(16, 4096, seed=5).cuda()
+    r = q(x)
+    y = torch.empty_like(r)
+    dt = L.dtype_code(x.dtype)
+    assert L.load().ts_qlinear_forward(ctypes.byref(v), x.data_ptr(), 16, 4096, dt, y.data_ptr(), 8192, dt, None,
+                                       None, 0, L.stream_ptr()) == L.TS_OK
+    assert float((y.float() - r.float()).abs().max() / r.float().abs().max()) <= 2e-3
 
 
 def test_reassigned_tensors_rebuild_the_view():
