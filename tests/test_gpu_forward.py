@@ -280,6 +280,46 @@ def test_forward_group_matches_single(opts):
             assert max_rel_err(y.float(), ref) <= TOL
 
 
+@pytest.mark.parametrize("opts", [dict(bits=2, group_size=64, outlier_frac=0.001, companded=True),
+                                  dict(bits=4, group_size=128, outlier_frac=0.001, companded=True, double_quant=True),
+                                  dict(bits=8, group_size=128, outlier_frac=0.001, companded=True)])
+def test_forward_group_per_layer_codebooks(opts):
+    """Lloyd-Max codebooks are fitted per tensor: a grouped launch builds each
+    workgroup's code table from its own layer's codebook (launch arguments up
+    to 16 entries, device memory beyond), so it must equal the per-layer
+    forwards."""
+    ts = _ts()
+    qls = []
+    for i, n in enumerate((384, 128, 200)):
+        torch.manual_seed(40 + i)  # Lloyd-Max samples from the global RNG
+        w = recipes.student_t_weight(n, 1024, 90 + i) if i != 1 else recipes.gaussian_weight(n, 1024, 90 + i)
+        qls.append(ts.QuantLinear(ts.quantize_tensor(w, **opts)))
+    cbs = [q.codebook.cpu() for q in qls]
+    assert not torch.equal(cbs[0], cbs[1]) and not torch.equal(cbs[1], cbs[2])
+    for M in (1, 4, 16):
+        x = recipes.activations(M, 1024, seed=M).cuda()
+        ys = ts.QuantLinear.forward_group(qls, x)
+        for q, y in zip(qls, ys):
+            assert max_rel_err(y.float(), q(x).float()) <= 1e-3, (M, q.out_features)
+
+
+@pytest.mark.parametrize("opts", [dict(bits=8, group_size=128, outlier_frac=0.002, double_quant=True, nf_quant=True),
+                                  dict(bits=2, group_size=64, outlier_frac=0.002, double_quant=True),
+                                  dict(bits=6, group_size=128, outlier_frac=0.002, double_quant=True),
+                                  dict(bits=4, group_size=32, outlier_frac=0.002, double_quant=False)])
+def test_forward_ragged_cols(opts):
+    """Columns a multiple of 8 but not of the group size (the last group is
+    partial and padded): decode (x chunks past the last column read as zero,
+    also in the per-group x sums at M = 1) and the prefill kernel."""
+    ql, W = _layer(200, 1000, 97, opts)
+    for M in (1, 3, 16, 40):
+        x = recipes.activations(M, 1000, seed=M).cuda()
+        ref = x.float() @ W.T
+        assert max_rel_err(ql(x).float(), ref) <= TOL, M
+        if M > 16:
+            assert max_rel_err(_forward_no_workspace(ql, x).float(), ref) <= TOL, ("fused", M)
+
+
 def test_forward_group_fallbacks():
     """Mixed formats and M > 16 run one forward per layer."""
     ts = _ts()
