@@ -109,7 +109,9 @@ size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M);
  * (modules.py:896-922): M <= 16 runs the HBM-bound decode kernel; M > 16
  * with a workspace of ts_forward_workspace_bytes(layer, M) bytes dequantizes
  * the layer into it and runs one hipBLASLt GEMM (bias in its epilogue);
- * otherwise the fused MFMA prefill kernel. x_dtype is TS_BF16 or TS_F16; bias
+ * otherwise the decode kernel on blocks of 16 tokens while that is the faster
+ * kernel for the shape (M <= 32; <= 64 on layers of <= 8192 rows; <= 128 on
+ * layers of <= 4096 rows), else the fused MFMA prefill kernel. x_dtype is TS_BF16 or TS_F16; bias
  * (may be NULL) has x_dtype. ldx/ldy are row strides in elements. Calls that
  * share a workspace must be ordered on one stream.
  */

@@ -2,6 +2,8 @@
 // include/tensorshrink_hip.h). Argument checking and dispatch only; the
 // kernels live in ts_decode.hip, ts_prefill.hip, ts_gemm.hip, ts_aux.hip,
 // ts_quantize.hip.
+#include <algorithm>
+
 #include "ts_common.h"
 
 namespace ts {
@@ -24,6 +26,19 @@ int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, 
 // reference switches to dequantize + F.linear above 64 rows; measured here the
 // GEMM path is faster than the fused MFMA kernel from 17 rows on).
 constexpr int64_t GEMM_MIN_M = 17;
+// Up to DEC_M_MAX rows of x the decode kernel runs them as blocks of 16
+// tokens that share each code-table read (the reference's fused kernel covers
+// M <= 64, modules.py:881-894). Above 16 rows it competes with the fused MFMA
+// prefill kernel, whose 256-row tiles leave most CUs idle at small M on
+// layers of few rows; measured on MI355X (4-bit, K = 4096 / 14336): decode
+// wins up to 32 rows on every shape, up to 64 rows on layers of at most 512
+// 16-row tiles, and up to 128 rows (two passes of 64) on layers of at most 256
+// tiles.
+constexpr int64_t DEC_M_MAX = 64;
+inline bool decode_mid_m(const ts_qlayer* L, int64_t M) {
+  const int64_t tiles = ts_cdiv(L->rows, 16);
+  return M <= 32 || (M <= 64 && tiles <= 512) || (M <= 2 * DEC_M_MAX && tiles <= 256);
+}
 int outlier_row_ptr(const int32_t* row, int64_t n, int64_t rows, int32_t* row_ptr, hipStream_t st);
 int tile_outlier_max(const int32_t* rp, int64_t rows, int32_t* out, hipStream_t st);
 int build_tile_outliers(const int32_t* rp, const int32_t* orow, const int32_t* ocol, const uint16_t* odelta,
@@ -110,8 +125,17 @@ int ts_qlinear_forward(const ts_qlayer* L, const void* x, int64_t M, int64_t ldx
   if (M >= ts::GEMM_MIN_M && workspace)
     rc = ts::gemm_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, workspace, workspace_bytes, S(stream));
   if (rc == TS_NOT_COVERED && aligned) {
-    if (M <= 16) rc = ts::decode_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
-    else rc = ts::prefill_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
+    if (M <= 16 || ts::decode_mid_m(L, M)) {
+      // passes of at most DEC_M_MAX rows; the first pass decides coverage
+      // (the format checks run before any launch)
+      const size_t ybytes = y_dtype == TS_F32 ? 4 : 2;
+      for (int64_t m0 = 0; m0 < M; m0 += ts::DEC_M_MAX) {
+        rc = ts::decode_forward(L, xp + m0 * ldx, std::min(ts::DEC_M_MAX, M - m0), ldx, x_dtype,
+                                static_cast<char*>(y) + m0 * ldy * ybytes, ldy, y_dtype, bp, S(stream));
+        if (rc != TS_OK) break;
+      }
+    }
+    if (rc == TS_NOT_COVERED && M > 16) rc = ts::prefill_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
   }
   if (rc == TS_NOT_COVERED) rc = ts::generic_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
   return rc;

@@ -1,4 +1,5 @@
-// Decode (M <= 16) quantized linear: y[M, N] = x[M, K] W^T + outliers + bias.
+// Decode (M <= 16, and up to 64 in MB blocks of 16 tokens) quantized linear:
+// y[M, N] = x[M, K] W^T + outliers + bias.
 //
 // Replaces the reference's fused Triton GEMV/skinny-GEMM
 // (triton_kernels.py:278-541, dispatched at modules.py:881-894) and its
@@ -9,7 +10,9 @@
 // batches. Layers that read the same x can share a launch (DecodeGroup).
 //   * MFMA f32_16x16x32 (bf16 or f16): lane l owns W row r0 + l%16 (B column)
 //     and x row l%16 (A row); lane group q = l/16 owns a quarter of each group,
-//     so one group is GS/32 MFMAs over that lane set.
+//     so one group is GS/32 MFMAs over that lane set. MB > 1: block tb's x
+//     rows 16 tb + l%16, with the group's code-table entries read once for
+//     all blocks.
 //   * Each lane loads its quarter-group of packed codes with 8/16-byte loads,
 //     U groups per batch, two batches in registers. A batch's per-group
 //     metadata comes in a few vector loads: U scale/double-quant codes in one
@@ -219,7 +222,7 @@ struct DecGeom {
 // Occupancy: at most 128 VGPRs (4 waves per SIMD, 16 per CU), so 1024 waves
 // of 16-row tiles are resident at once across 256 CUs.
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
-          int NB, int RT>
+          int NB, int RT, int MB>
 __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) {
   constexpr int NT = 64 * W;
   constexpr bool LOOP = NB == 0;
@@ -276,8 +279,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   if constexpr (USE_T4) { t4 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
   if constexpr (USE_T2) { t2 = reinterpret_cast<uint2*>(sp); sp += 256 * R * 8; }
   if constexpr (USE_T8) { t8 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
-  float* red = reinterpret_cast<float*>(sp);       // [RT][W][64][4]
-  sp += RT * W * 64 * 4 * 4;
+  float* red = reinterpret_cast<float*>(sp);       // [MB][RT][W][64][4]
+  sp += MB * RT * W * 64 * 4 * 4;
   float* cbs = reinterpret_cast<float*>(sp);       // [256] staged codebook
   sp += 256 * 4;
   // XM_SLOT: each wave's x slot (64 lanes x 16 bytes)
@@ -421,7 +424,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
 
   auto load_batch = [&](int64_t tile, int b, Batch& B) { load_batch_of(a, tile, b, B); };
 
-  // float32 (scale, gmin) of group u of a batch
+  // Codebook tables (4-bit, and 2-bit outside RVQ) hold cb[c] - c0, c0 the
+  // middle of the codebook's range, and the offset term takes gmin + c0 s:
+  // the same affine, with the bf16 rounding of the table entries halved for
+  // codebooks on [0, 2^b - 1] (NF, Lloyd-Max). Uniform grids keep c0 = 0.
+  constexpr bool CENTER = !RVQ && (BITS == 4 || BITS == 2);
+  float c0 = 0.f;
+  // float32 (scale, gmin + c0 scale) of group u of a batch
   auto group_affine = [&](const Batch& B, int u, float& s_, float& gm_) {
     if constexpr (DQ) {  // modules.py:573-579: code * meta_scale + meta_min in float32
       const float cs = (float)(AL ? byte_of(B.sc, u) : B.sc[u]);
@@ -434,9 +443,10 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       s_ = ts_h2f((uint16_t)(AL ? half_of(B.sc, u) : B.sc[u]));
       gm_ = ts_h2f((uint16_t)(AL ? half_of(B.gc, u) : B.gc[u]));
     }
+    if constexpr (CENTER) gm_ = __builtin_fmaf(c0, s_, gm_);
   };
 
-  auto compute_batch = [&](int b, const Batch& B, ts_f32x4& yacc) {
+  auto compute_batch = [&](int b, const Batch& B, ts_f32x4* yacc) {
     // M = 1: the batch's x chunks go to this wave's LDS slot once; each MFMA
     // then reads its chunk back with the 16 lanes of a row on one address (a
     // broadcast read), instead of moving it with DPP (VALU) per MFMA. Reads
@@ -507,11 +517,11 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
             xa[j] = *reinterpret_cast<const ts_u32x4*>(xw + (16 * q + u * NMF + j) * 8);
           } else if constexpr (XLDS) {
             xa[j] = *reinterpret_cast<const ts_u32x4*>(xrow_lds + col);
-          } else {
+          } else if constexpr (MB == 1) {
             const ts_u32x4 v = ts_ld16(xrow_glb + min(col, (int)a.cols - 8));
             xa[j] = col < a.cols ? v : ts_u32x4{0u, 0u, 0u, 0u};
           }
-        } else {
+        } else if constexpr (XM == XM_SLOT || XLDS || MB == 1) {
           ts_u32x2 v;
           if constexpr (XM == XM_SLOT) {
             v = *reinterpret_cast<const ts_u32x2*>(xw + (16 * q + u * NMF + j) * 4);
@@ -556,35 +566,58 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
           bv2[j] = ts_u32x4{e0.x, e0.y, e1.x, e1.y};
         }
       }
-      // Phase 2: the group's MFMAs (ax: per-row sums of x over the group).
-      ts_f32x4 aw = {0.f, 0.f, 0.f, 0.f};
-      ts_f32x4 ax = {0.f, 0.f, 0.f, 0.f};
-      ts_f32x4 aw2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < NMF; ++j) {
-        aw = ts_mfma16x16x32<BF16>(xa[j], bv[j], aw);
-        if constexpr (XM != XM_SLOT) ax = ts_mfma16x16x32<BF16>(xa[j], ones, ax);
-        if constexpr (RVQ) aw2 = ts_mfma16x16x32<BF16>(xa[j], bv2[j], aw2);
-      }
-      if constexpr (XM == XM_SLOT)
-        ax[0] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, xsum), u * NMF));
       float s2_ = 0.f, g2_ = 0.f;
       if constexpr (RVQ) {
         s2_ = ts_h2f((uint16_t)(AL ? half_of(B.s2s, u) : B.s2s[u]));
         g2_ = ts_h2f((uint16_t)(AL ? half_of(B.s2g, u) : B.s2g[u]));
       }
-      // M = 1 (XM_SLOT): only element 0 of lanes 0-15 (token 0) is stored
-      constexpr int NI = XM == XM_SLOT ? 1 : 4;
+      // Phase 2: the group's MFMAs (ax: per-row sums of x over the group),
+      // for each block of 16 tokens (MB > 1: x of block tb read from global
+      // memory here; the code-table entries above serve every block).
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        float v = yacc[i];
-        v = __builtin_fmaf(s_, aw[i], v);
-        v = __builtin_fmaf(gm_, ax[i], v);
-        if constexpr (RVQ) {
-          v = __builtin_fmaf(s2_, aw2[i], v);
-          v = __builtin_fmaf(g2_, ax[i], v);
+      for (int tb = 0; tb < MB; ++tb) {
+        if constexpr (MB > 1) {
+          const uint16_t* xr = a.x + (int64_t)min(16 * tb + n, a.M - 1) * a.ldx;
+#pragma unroll
+          for (int j = 0; j < NMF; ++j) {
+            const int col = c0 + j * CPM;
+            if constexpr (CPM == 8) {
+              const ts_u32x4 v = ts_ld16(xr + min(col, (int)a.cols - 8));
+              xa[j] = col < a.cols ? v : ts_u32x4{0u, 0u, 0u, 0u};
+            } else {
+              const ts_u32x2 l = ts_ld8(xr + min(col, (int)a.cols - 4));
+              const ts_u32x2 v = col < a.cols ? l : ts_u32x2{0u, 0u};
+              xa[j] = ts_u32x4{__builtin_amdgcn_perm(v.x, v.x, 0x05040100u),
+                               __builtin_amdgcn_perm(v.x, v.x, 0x07060302u),
+                               __builtin_amdgcn_perm(v.y, v.y, 0x05040100u),
+                               __builtin_amdgcn_perm(v.y, v.y, 0x07060302u)};
+            }
+          }
         }
-        yacc[i] = v;
+        ts_f32x4 aw = {0.f, 0.f, 0.f, 0.f};
+        ts_f32x4 ax = {0.f, 0.f, 0.f, 0.f};
+        ts_f32x4 aw2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NMF; ++j) {
+          aw = ts_mfma16x16x32<BF16>(xa[j], bv[j], aw);
+          if constexpr (XM != XM_SLOT) ax = ts_mfma16x16x32<BF16>(xa[j], ones, ax);
+          if constexpr (RVQ) aw2 = ts_mfma16x16x32<BF16>(xa[j], bv2[j], aw2);
+        }
+        if constexpr (XM == XM_SLOT)
+          ax[0] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, xsum), u * NMF));
+        // M = 1 (XM_SLOT): only element 0 of lanes 0-15 (token 0) is stored
+        constexpr int NI = XM == XM_SLOT ? 1 : 4;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          float v = yacc[tb][i];
+          v = __builtin_fmaf(s_, aw[i], v);
+          v = __builtin_fmaf(gm_, ax[i], v);
+          if constexpr (RVQ) {
+            v = __builtin_fmaf(s2_, aw2[i], v);
+            v = __builtin_fmaf(g2_, ax[i], v);
+          }
+          yacc[tb][i] = v;
+        }
       }
     }
   };
@@ -638,7 +671,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // ---- one tile per workgroup, batches double-buffered ----------------------
   if (tile >= a.n_tiles) return;
   const int64_t r0 = tile * 16;
-  ts_f32x4 yacc = {0.f, 0.f, 0.f, 0.f};
+  ts_f32x4 yacc[MB];
+#pragma unroll
+  for (int tb = 0; tb < MB; ++tb) yacc[tb] = ts_f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Every load of the tile is issued up front, none depending on another: x
   // chunks, the codebook, both weight batches, the tile's outlier slots and
@@ -737,12 +772,15 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
   }
   ts_lds_barrier();
+  if constexpr (CENTER) {
+    if (a.cb_mode != CB_UNIFORM) c0 = 0.5f * (cbs[0] + cbs[NCB - 1]);
+  }
   // entry b's R copies are contiguous: 16-byte stores of four (u32 entries)
   // or two (u64 entries) copies at a time
   if constexpr (USE_T4 && !USE_T2 && R % 4 == 0) {
     for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
       const int b = e / R;
-      const uint32_t v = pack2<BF16>(cbs[b & 15], cbs[b >> 4]);
+      const uint32_t v = pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
       *reinterpret_cast<ts_u32x4*>(t4 + e) = ts_u32x4{v, v, v, v};
     }
   } else if constexpr (USE_T8 && R % 4 == 0) {
@@ -757,20 +795,20 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     for (int e = 2 * tid; e < 256 * R; e += 2 * NT) {
       const int b = e / R;
       float v[4];
-      for (int j = 0; j < 4; ++j) v[j] = cbs[(b >> (2 * j)) & 3];  // a 2-bit layer's codebook
+      for (int j = 0; j < 4; ++j) v[j] = cbs[(b >> (2 * j)) & 3] - c0;  // a 2-bit layer's codebook
       const uint32_t lo = pack2<BF16>(v[0], v[1]), hi = pack2<BF16>(v[2], v[3]);
       *reinterpret_cast<ts_u32x4*>(t2 + e) = ts_u32x4{lo, hi, lo, hi};
     }
   } else
   for (int e = tid; e < 256 * R; e += NT) {
     const int b = e / R;
-    if constexpr (USE_T4) t4[e] = pack2<BF16>(cbs[b & 15], cbs[b >> 4]);
+    if constexpr (USE_T4) t4[e] = pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
     if constexpr (USE_T2) {
       // RVQ stage 2 is always a uniform grid; a 2-bit layer uses its codebook.
       float v[4];
       for (int j = 0; j < 4; ++j) {
         const int c = (b >> (2 * j)) & 3;
-        v[j] = RVQ ? (float)c : cbs[c];
+        v[j] = RVQ ? (float)c : cbs[c] - c0;
       }
       t2[e] = make_uint2(pack2<BF16>(v[0], v[1]), pack2<BF16>(v[2], v[3]));
     }
@@ -783,6 +821,12 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   }
   ts_lds_barrier();
 
+  // Offset of (token m, tile row) in a wave's partials: block m / 16 of
+  // [MB][W][64][4], lane row + 16 (m % 16 / 4), element m % 4 (the MFMA's D
+  // layout).
+  auto pidx = [&](int m, uint32_t row) {
+    return (m >> 4) * (W * 256) + (int)(row + 16 * ((m & 15) >> 2)) * 4 + (m & 3);
+  };
   // The tile's outliers through the CSR row offsets (csr layers), added into
   // the wave's partials rw like the slots: the tile's rows own one
   // contiguous range of the row-sorted tables.
@@ -795,7 +839,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       const float d = ts_h2f(C.delta[i]);
       for (int m = 0; m < A.M; ++m) {
         const float xv = XLDS ? XT<BF16>::to_f(xs[m * A.K + col]) : XT<BF16>::to_f(A.x[(int64_t)m * A.ldx + col]);
-        atomicAdd(&rw[(row + 16 * (m >> 2)) * 4 + (m & 3)], xv * d);
+        atomicAdd(&rw[pidx(m, row)], xv * d);
       }
     }
   };
@@ -854,8 +898,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     const uint16_t b0v = load_bias(tile), b1v = load_bias(t1);
     asm volatile("" ::: "memory");
     ts_f32x4 y1 = {0.f, 0.f, 0.f, 0.f};
-    compute_batch2(0, bufA, bufB, yacc, y1);
-    epilogue(tile, yacc, s00, b0v, 0);
+    compute_batch2(0, bufA, bufB, yacc[0], y1);
+    epilogue(tile, yacc[0], s00, b0v, 0);
     if (live1) epilogue(t1, y1, s10, b1v, 1);
     return;
   }
@@ -866,9 +910,10 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // barrier before the cross-wave sum covers them too. Entry of token m, row
   // nn: lane nn + 16 (m / 4), element m % 4 (the MFMA's D layout). rb: the
   // partials buffer ([W][64][4]).
-  auto epilogue_of = [&](const DecodeArgs& A, int64_t t, const ts_f32x4& yv, uint64_t slot0, uint16_t bias_v,
+  auto epilogue_of = [&](const DecodeArgs& A, int64_t t, const ts_f32x4* yv, uint64_t slot0, uint16_t bias_v,
                          float* rb) {
-    *reinterpret_cast<ts_f32x4*>(rb + (wave * 64 + lane) * 4) = yv;
+#pragma unroll
+    for (int tb = 0; tb < MB; ++tb) *reinterpret_cast<ts_f32x4*>(rb + tb * (W * 256) + (wave * 64 + lane) * 4) = yv[tb];
     if (A.cap > 0) {
       // slot = col | (row in tile) << 32 | f16 delta << 48; a zero delta (an
       // unused slot) adds nothing and is skipped
@@ -880,7 +925,7 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
         const float d = ts_h2f((uint16_t)dbits);
         for (int m = 0; m < A.M; ++m) {
           const float xv = XLDS ? XT<BF16>::to_f(xs[m * A.K + col]) : XT<BF16>::to_f(A.x[(int64_t)m * A.ldx + col]);
-          atomicAdd(&rw[(row + 16 * (m >> 2)) * 4 + (m & 3)], xv * d);
+          atomicAdd(&rw[pidx(m, row)], xv * d);
         }
       };
       if (tid < A.cap) add_slot(slot0);
@@ -889,14 +934,15 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       add_csr(A, t, rb + wave * 64 * 4);
     }
     ts_lds_barrier();
-    // the tile's 16 x 16 (token m, row nn) outputs: the thread that sums one
-    // over the waves also adds the bias and stores it
-    if (tid < 256) {
-      const int l = tid >> 2, i = tid & 3;
+    // the tile's 16 x 16 MB (token m, row nn) outputs: the thread that sums
+    // one over the waves also adds the bias and stores it (one output per
+    // thread: 256 MB <= NT wherever MB > 1)
+    if (tid < 256 * MB) {
+      const int tb = tid >> 8, l = (tid >> 2) & 63, i = tid & 3;
       float acc = 0.f;
 #pragma unroll
-      for (int w = 0; w < W; ++w) acc += rb[(w * 64 + l) * 4 + i];
-      const int m = 4 * (l >> 4) + i, nn = l & 15;
+      for (int w = 0; w < W; ++w) acc += rb[tb * (W * 256) + (w * 64 + l) * 4 + i];
+      const int m = 16 * tb + 4 * (l >> 4) + i, nn = l & 15;
       const int64_t r = t * 16 + nn;
       if (m < A.M && r < A.N) {
         if (A.bias_mul) acc += XT<BF16>::to_f(bias_v);
@@ -954,14 +1000,14 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   epilogue_of(a, tile, yacc, slot0, bias_v, red);
 }
 
-template <int BITS, bool CB8, bool RVQ, int REP, int XM, int W, int RT>
+template <int BITS, bool CB8, bool RVQ, int REP, int XM, int W, int RT, int MB = 1>
 inline size_t decode_smem(int M, int64_t K, bool xlds) {
   constexpr int R = dec_rep_x(REP, W, XM);
   size_t s = 0;
   if (BITS == 4) s += 256 * R * 4;
   if (BITS == 2 || RVQ) s += 256 * R * 8;
   if (BITS == 8 && CB8) s += 256 * R * 4;
-  s += (size_t)RT * W * 64 * 16;
+  s += (size_t)MB * RT * W * 64 * 16;
   s += 256 * 4;
   if (XM == XM_SLOT) s += (size_t)W * 1024;
   if (xlds) s += ((size_t)M * K * 2 + 1023) / 1024 * 1024;  // whole 1 KB chunks
@@ -969,7 +1015,7 @@ inline size_t decode_smem(int M, int64_t K, bool xlds) {
 }
 
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP, int XM, bool DQ, bool AL, int W, int U,
-          int NB, int RT = 1>
+          int NB, int RT = 1, int MB = 1>
 inline int launch_decode_x(const DecodeGroup& g_in, hipStream_t st) {
   // RT row tiles per workgroup: tile_end becomes the cumulative workgroup count
   DecodeGroup g = g_in;
@@ -981,8 +1027,8 @@ inline int launch_decode_x(const DecodeGroup& g_in, hipStream_t st) {
     }
   }
   const DecodeArgs& a = g.a[0];
-  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, XM, W, RT>(a.M, a.K, XM != XM_GLOBAL && XM != XM_SLOT);
-  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB, RT>;
+  const size_t smem = decode_smem<BITS, CB8, RVQ, REP, XM, W, RT, MB>(a.M, a.K, XM != XM_GLOBAL && XM != XM_SLOT);
+  auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB, RT, MB>;
   static std::once_flag flags[64];
   static bool ok[64];
   if (!ts_set_smem_once(reinterpret_cast<const void*>(kern), 160 * 1024, flags, ok)) return TS_HIP_ERROR;
@@ -1023,6 +1069,7 @@ inline DecShape decode_shape(int64_t n_tiles, int64_t G, int umax) {
 template <int BITS, int GS, bool BF16, bool CB8, bool RVQ, int REP>
 inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   constexpr int UMAX = DecGeom<BITS, GS, RVQ>::UMAX;
+  constexpr int UMB = UMAX >= 2 ? UMAX / 2 : 1;  // batches of the multi-block (M > 16) launches: registers
   const DecodeArgs& a = g.a[0];
   const bool xlds = (size_t)a.M * a.K * 2 <= DEC_XLDS_MAX;
   const bool dq = a.dqsc != nullptr;
@@ -1062,11 +1109,22 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, (LP) ? 0 : 2>(g, st)
 #define TS_DEC1(XMV, DQV, ALV, WV, UV) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, 1>(g, st)
+#define TS_DECMB(DQV, ALV, MBV) \
+  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XM_GLOBAL, DQV, ALV, 16, UMB, 0, 1, MBV>(g, st)
 #define TS_DECRT(DQV, WV) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XM_GLOBAL, DQV, true, WV, UMAX, 1, 2>(g, st)
 #define TS_DEC_ALL(DQV)                                                          \
   do {                                                                           \
     const bool alm = aligned(UMAX);                                              \
+    if (a.M > 16) { /* blocks of 16 tokens share each code-table read */          \
+      if (a.M > 64) return TS_NOT_COVERED;                                       \
+      if (a.M <= 32) {                                                           \
+        if (alm) TS_DECMB(DQV, true, 2);                                         \
+        TS_DECMB(DQV, false, 2);                                                 \
+      }                                                                          \
+      if (alm) TS_DECMB(DQV, true, 4);                                           \
+      TS_DECMB(DQV, false, 4);                                                   \
+    }                                                                            \
     if constexpr (SLOT_OK) {                                                      \
       if (slot && sh.ok && alm) {                                                 \
         if (sh.W == 4) {                                                         \
@@ -1110,6 +1168,7 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   TS_DEC_ALL(false);
 #undef TS_DEC_ALL
 #undef TS_DECRT
+#undef TS_DECMB
 #undef TS_DEC1
 #undef TS_DEC
 }

@@ -134,7 +134,7 @@ def fused_quantized_linear(
         s.stage2_packed, s.stage2_stride = stage2_packed.data_ptr(), stage2_packed.shape[1]
         s.stage2_scale, s.stage2_gmin = stage2_scale.data_ptr(), stage2_gmin.data_ptr()
     if outlier_row is not None and outlier_row.numel() > 0:
-        ent = _derived_outliers(outlier_row, outlier_col, outlier_delta, out_features, need_slots=M <= 16)
+        ent = _derived_outliers(outlier_row, outlier_col, outlier_delta, out_features, need_slots=M <= 128)
         s.outlier_row, s.outlier_col = outlier_row.data_ptr(), outlier_col.data_ptr()
         s.outlier_delta, s.n_outliers = outlier_delta.data_ptr(), outlier_row.numel()
         s.outlier_row_ptr = ent["rp"].data_ptr()

@@ -5,7 +5,8 @@ Drop-in for modules.py of GDNickk/tensorshrink v0.4.0: ``QuantLinear``
 and contents (packed, scale/gmin or dq_*, codebook, outlier_row/col sorted by
 row, outlier_delta, bias), and ``quantize_module`` (modules.py:1258-1455) takes
 the same arguments. The forward runs one libtensorshrink_hip launch per call
-(decode kernel for M <= 16, MFMA prefill kernel above), with the outlier
+(decode kernel for M <= 16 and small M on short layers, MFMA prefill kernel
+above), with the outlier
 correction and bias fused; there is no CPU or PyTorch fallback path.
 
 Additions over the reference:
@@ -376,8 +377,9 @@ class QuantLinear(nn.Module):
         b = self._bias_as(in_dtype)
         dt = L.dtype_code(in_dtype)
         lib = L.load()
-        # no workspace: M <= 16 runs the decode kernel, larger M the fused
-        # dequant-into-LDS MFMA kernel
+        # no workspace: the decode kernel (M <= 16, and blocks of 16 tokens
+        # up to 32-128 rows by layer height), else the fused dequant-into-LDS
+        # MFMA kernel
         with torch.cuda.device(x.device):
             L.check(lib.ts_qlinear_forward(ctypes.byref(self._layer), x2d.data_ptr(), M, self.in_features, dt,
                                            y.data_ptr(), self.out_features, dt, L.ptr(b), None, 0,

@@ -320,6 +320,28 @@ def test_forward_ragged_cols(opts):
             assert max_rel_err(_forward_no_workspace(ql, x).float(), ref) <= TOL, ("fused", M)
 
 
+@pytest.mark.parametrize("opts", [NF4, dict(bits=8, group_size=128, outlier_frac=0.002, double_quant=True, nf_quant=True),
+                                  dict(bits=2, group_size=64, outlier_frac=0.002, double_quant=True),
+                                  dict(bits=6, group_size=128, outlier_frac=0.002, double_quant=True)])
+def test_forward_mid_m(opts):
+    """17 to 128 rows of x on a layer of few row tiles: the decode kernel's
+    blocks of 16 tokens (passes of 64 rows above 64), through QuantLinear and
+    through the C-ABI with a float32 output of row stride past N."""
+    from tensorshrink_amd import _lib as L
+    ql, W = _layer(256, 1024, 98, opts)
+    ql.bias = (torch.randn(256, generator=torch.Generator().manual_seed(4)) * 0.1).to(torch.bfloat16).cuda()
+    for M in (17, 32, 33, 48, 64, 65, 100, 128):
+        x = recipes.activations(M, 1024, seed=M).cuda()
+        ref = x.float() @ W.T + ql.bias.float()
+        assert max_rel_err(ql(x).float(), ref) <= TOL, M
+        ldy = 300
+        y = torch.full((M, ldy), 7.0, dtype=torch.float32, device="cuda")
+        L.check(L.load().ts_qlinear_forward(ctypes.byref(ql._layer), x.data_ptr(), M, 1024, L.TS_BF16, y.data_ptr(),
+                                            ldy, L.TS_F32, ql.bias.data_ptr(), None, 0, L.stream_ptr()), "fwd")
+        assert max_rel_err(y[:, :256], ref) <= TOL, ("f32", M)
+        assert bool((y[:, 256:] == 7.0).all()), M  # the stride's tail is untouched
+
+
 def test_forward_group_fallbacks():
     """Mixed formats and M > 16 run one forward per layer."""
     ts = _ts()
