@@ -121,7 +121,7 @@ int ts_qlinear_forward(const ts_qlayer* layer, const void* x, int64_t M, int64_t
 
 /*
  * The forward above for n (1..4) layers that read the same x (q/k/v, gate/up)
- * in one launch: y[l][M, rows_l] = x @ W_l^T (+ bias[l]). Covers M <= 16 with
+ * in one launch: y[l][M, rows_l] = x @ W_l^T (+ bias[l]). Covers M <= 32 with
  * layers of one format (bits, group size, cols, codebook / double-quant /
  * stage-2 kind); returns TS_NOT_COVERED otherwise, and the caller runs
  * ts_qlinear_forward per layer. No counterpart in the reference, which calls

@@ -155,7 +155,7 @@ int ts_qlinear_forward_group(const ts_qlayer* const* layers, int n_layers, const
   if (M == 0) return TS_OK;
   const ts_qlayer* L0 = layers[0];
   const bool aligned = (L0->cols % 8 == 0) && (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
-  if (!aligned || M > 16) return TS_NOT_COVERED;
+  if (!aligned || M > 32) return TS_NOT_COVERED;  // (decode wins up to 32 rows on every shape)
   return ts::decode_forward_group(layers, n_layers, static_cast<const uint16_t*>(x), M, ldx, x_dtype, y, ldy, y_dtype,
                                   reinterpret_cast<const uint16_t* const*>(bias), S(stream));
 }

@@ -389,7 +389,7 @@ class QuantLinear(nn.Module):
     @staticmethod
     def forward_group(layers: Sequence["QuantLinear"], x: torch.Tensor) -> List[torch.Tensor]:
         """[layer(x) for layer in layers] in one kernel launch when the layers
-        share a format and the input has at most 16 rows (q/k/v or gate/up at
+        share a format and the input has at most 32 rows (q/k/v or gate/up at
         decode); otherwise, or when the launch is not covered, one forward per
         layer. No counterpart in the reference, whose model code calls each
         QuantLinear in turn (modules.py:896-905)."""
@@ -398,7 +398,7 @@ class QuantLinear(nn.Module):
         M = 1
         for d in x.shape[:-1]:
             M *= d
-        ok = (1 <= len(layers) <= 4 and M <= 16 and x.is_cuda and in_dtype in (torch.float16, torch.bfloat16)
+        ok = (1 <= len(layers) <= 4 and M <= 32 and x.is_cuda and in_dtype in (torch.float16, torch.bfloat16)
               and all(q._layer is not None and not q.force_fp32_compute and q.in_features == layers[0].in_features
                       for q in layers))
         if ok:

@@ -269,7 +269,7 @@ def test_forward_group_matches_single(opts):
     qls = [m[0] for m in made]
     torch.manual_seed(0)
     qls[1].bias = torch.randn(qls[1].out_features, dtype=torch.bfloat16).cuda()
-    for M in (1, 5, 16):
+    for M in (1, 5, 16, 24, 32):
         x = recipes.activations(M, 1024, seed=M).cuda()
         ys = ts.QuantLinear.forward_group(qls, x)
         for q, (ql, W), y in zip(qls, made, ys):
@@ -296,7 +296,7 @@ def test_forward_group_per_layer_codebooks(opts):
         qls.append(ts.QuantLinear(ts.quantize_tensor(w, **opts)))
     cbs = [q.codebook.cpu() for q in qls]
     assert not torch.equal(cbs[0], cbs[1]) and not torch.equal(cbs[1], cbs[2])
-    for M in (1, 4, 16):
+    for M in (1, 4, 16, 32):
         x = recipes.activations(M, 1024, seed=M).cuda()
         ys = ts.QuantLinear.forward_group(qls, x)
         for q, y in zip(qls, ys):
@@ -343,7 +343,7 @@ def test_forward_mid_m(opts):
 
 
 def test_forward_group_fallbacks():
-    """Mixed formats and M > 16 run one forward per layer."""
+    """Mixed formats and M > 32 run one forward per layer."""
     ts = _ts()
     a, Wa = _layer(256, 512, 81, NF4)
     b, Wb = _layer(256, 512, 82, dict(bits=8, group_size=128, outlier_frac=0.0, double_quant=False))
