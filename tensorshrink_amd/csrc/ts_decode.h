@@ -935,10 +935,10 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
     ts_lds_barrier();
     // the tile's 16 x 16 MB (token m, row nn) outputs: the thread that sums
-    // one over the waves also adds the bias and stores it (one output per
-    // thread: 256 MB <= NT wherever MB > 1)
-    if (tid < 256 * MB) {
-      const int tb = tid >> 8, l = (tid >> 2) & 63, i = tid & 3;
+    // one over the waves also adds the bias and stores it (thread tid takes
+    // outputs tid + k NT, all of row nn = (tid / 4) % 16, whose bias it holds)
+    for (int e = tid; e < 256 * MB; e += NT) {
+      const int tb = e >> 8, l = (e >> 2) & 63, i = e & 3;
       float acc = 0.f;
 #pragma unroll
       for (int w = 0; w < W; ++w) acc += rb[tb * (W * 256) + (w * 64 + l) * 4 + i];
@@ -1109,8 +1109,12 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, (LP) ? 0 : 2>(g, st)
 #define TS_DEC1(XMV, DQV, ALV, WV, UV) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, 1>(g, st)
-#define TS_DECMB(DQV, ALV, MBV) \
-  return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XM_GLOBAL, DQV, ALV, 16, UMB, 0, 1, MBV>(g, st)
+#define TS_DECMB(DQV, ALV, MBV)                                                                      \
+  do {                                                                                               \
+    if (g.tile_end[g.n - 1] > 512)                                                                   \
+      return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XM_GLOBAL, DQV, ALV, 4, UMB, 0, 1, MBV>(g, st); \
+    return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XM_GLOBAL, DQV, ALV, 16, UMB, 0, 1, MBV>(g, st);  \
+  } while (0)
 #define TS_DECRT(DQV, WV) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XM_GLOBAL, DQV, true, WV, UMAX, 1, 2>(g, st)
 #define TS_DEC_ALL(DQV)                                                          \

@@ -342,6 +342,16 @@ def test_forward_mid_m(opts):
         assert bool((y[:, 256:] == 7.0).all()), M  # the stride's tail is untouched
 
 
+def test_forward_mid_m_many_tiles():
+    """The multi-block decode launches of more than 512 row tiles (4-wave
+    workgroups, each wave streaming several batches; outputs looped over the
+    workgroup's threads)."""
+    ql, W = _layer(8320, 256, 99, NF4)
+    for M in (20, 33):
+        x = recipes.activations(M, 256, seed=M).cuda()
+        assert max_rel_err(ql(x).float(), x.float() @ W.T) <= TOL, M
+
+
 def test_forward_group_fallbacks():
     """Mixed formats and M > 32 run one forward per layer."""
     ts = _ts()
