@@ -10,7 +10,8 @@
 //
 // Tiles of 256 x BN x 64. BN = 256 (when the tiles fill the CUs): 8 waves,
 // two per SIMD, as a 2 x 4 grid of 128 x 64 wave tiles (4 x 2 MFMA blocks of
-// 32 x 32); BN = 128: 4 waves, one per SIMD, 2 x 2 grid of 128 x 64. Each
+// 32 x 32); BN = 128: 4 waves, one per SIMD, 2 x 2 grid of 128 x 64 (or of
+// 64 x 64 with 128-row tiles, when 256-row tiles would leave CUs idle). Each
 // weight element is dequantized once per workgroup. Sized from gfx950
 // measurements: a 32x32x16 MFMA occupies a SIMD for 32 cycles; the LDS serves
 // ds_read_b128 at about 190 B per cycle, ds_write_b128 at half that, and a
@@ -129,11 +130,11 @@ TS_DEV int64_t xcd_tile(int64_t b, int64_t n) {
   return x * q + min(x, r) + i;
 }
 
-template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN, int NW>
+template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN, int NW, int BM>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a_in) {
-  constexpr int BM = PF_BM, BK = PF_BK, NT = 64 * NW;
+  constexpr int BK = PF_BK, NT = 64 * NW;
   constexpr int WN = NW / 2;                    // waves along N (two along M)
-  constexpr int TM = 4;                         // 32-row blocks per wave along M (128 rows)
+  constexpr int TM = BM / 64;                   // 32-row blocks per wave along M (BM / 2 rows)
   constexpr int TN = BN / (32 * WN);            // 32-column blocks per wave along N
   constexpr int TPR = NT / BN;                  // threads per weight row (1 or 2)
   constexpr int CPT = BK / TPR;                 // weight codes per thread per k-step (64 or 32)
@@ -600,28 +601,29 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   }
 }
 
-template <int BITS, bool CB, int BN>
+template <int BITS, bool CB, int BN, int BM>
 constexpr size_t prefill_smem() {
   constexpr int CBN = CB ? (1 << BITS) : 0;
-  return (size_t)2 * (PF_BM + BN) * PF_BK * 2 + (size_t)CBN * 32 * 4;
+  return (size_t)2 * (BM + BN) * PF_BK * 2 + (size_t)CBN * 32 * 4;
 }
 
-template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN, int NW>
+template <int BITS, int GS, bool BF16, bool CB, bool RVQ, bool DQ, int BN, int NW, int BM = PF_BM>
 inline int launch_prefill(PrefillArgs a, hipStream_t st) {
-  constexpr size_t smem = prefill_smem<BITS, CB, BN>();
+  constexpr size_t smem = prefill_smem<BITS, CB, BN, BM>();
   static_assert(smem <= 160 * 1024, "LDS budget (160 KB per CU)");
-  auto kern = prefill_kernel<BITS, GS, BF16, CB, RVQ, DQ, BN, NW>;
+  auto kern = prefill_kernel<BITS, GS, BF16, CB, RVQ, DQ, BN, NW, BM>;
   static std::once_flag flags[64];
   static bool ok[64];
   if (!ts_set_smem_once(reinterpret_cast<const void*>(kern), smem, flags, ok)) return TS_HIP_ERROR;
-  a.m_tiles = ts_cdiv(a.M, PF_BM);
+  a.m_tiles = ts_cdiv(a.M, BM);
   a.n_tiles = ts_cdiv(a.N, BN);
   hipLaunchKernelGGL(kern, dim3((unsigned)(a.m_tiles * a.n_tiles)), dim3(64 * NW), smem, st, a);
   TS_CHECK_LAUNCH();
   return TS_OK;
 }
 
-// 256 x 256 tiles when they fill the CUs, else 256 x 128.
+// 256 x 256 tiles when they fill the CUs, else 256 x 128, or 128 x 128 when
+// those would still leave CUs idle and 128 x 128 tiles fit one round.
 template <int BITS, int GS, bool BF16, bool CB, bool RVQ>
 inline int launch_prefill_tiles(PrefillArgs& a, hipStream_t st) {
   const bool dq = a.dqsc != nullptr;
@@ -629,6 +631,12 @@ inline int launch_prefill_tiles(PrefillArgs& a, hipStream_t st) {
   if (wide) {
     return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 256, PF_NW_WIDE>(a, st)
               : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 256, PF_NW_WIDE>(a, st);
+  }
+  // 128-row tiles when they still fit one round of workgroups: twice the
+  // workgroups of 256-row tiles (or half their padding at M <= 128)
+  if (ts_cdiv(a.M, PF_BM) * ts_cdiv(a.N, 128) < 256 && ts_cdiv(a.M, 128) * ts_cdiv(a.N, 128) <= 256) {
+    return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, 4, 128>(a, st)
+              : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128, 4, 128>(a, st);
   }
   return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, 4>(a, st)
             : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128, 4>(a, st);

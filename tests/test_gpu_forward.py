@@ -343,11 +343,12 @@ def test_forward_mid_m(opts):
 
 
 def test_forward_mid_m_many_tiles():
-    """The multi-block decode launches of more than 512 row tiles (4-wave
-    workgroups, each wave streaming several batches; outputs looped over the
-    workgroup's threads)."""
+    """Small M on a layer of 520 row tiles: the multi-block decode launch
+    (M = 20: 4-wave workgroups, each wave streaming several batches, outputs
+    looped over the workgroup's threads) and the prefill kernel's 128-row
+    tiles (M = 33, 100, 200)."""
     ql, W = _layer(8320, 256, 99, NF4)
-    for M in (20, 33):
+    for M in (20, 33, 100, 200):
         x = recipes.activations(M, 256, seed=M).cuda()
         assert max_rel_err(ql(x).float(), x.float() @ W.T) <= TOL, M
 
