@@ -353,6 +353,32 @@ def test_forward_mid_m_many_tiles():
         assert max_rel_err(ql(x).float(), x.float() @ W.T) <= TOL, M
 
 
+def test_forward_random_shapes():
+    """A seeded sweep over formats, shapes and batch sizes, so every dispatch
+    boundary (decode, its token blocks and passes, the prefill tile shapes,
+    ragged columns, the generic kernel) meets the dequantized weight's
+    float32 product."""
+    ts = _ts()
+    rng = np.random.default_rng(1234)
+    fmts = [dict(bits=4, group_size=128, double_quant=True, nf_quant=True), dict(bits=4, group_size=64),
+            dict(bits=4, group_size=32, double_quant=True), dict(bits=8, group_size=128, nf_quant=True),
+            dict(bits=8, group_size=64, double_quant=True), dict(bits=2, group_size=64, double_quant=True),
+            dict(bits=2, group_size=128), dict(bits=6, group_size=128, double_quant=True), dict(bits=6, group_size=64)]
+    for case in range(36):
+        opts = dict(fmts[case % len(fmts)])
+        opts["outlier_frac"] = float(rng.choice([0.0, 0.001, 0.01]))
+        rows = int(rng.integers(16, 5200))
+        cols = int(rng.choice([8 * int(rng.integers(8, 400)), int(rng.integers(64, 3000))]))
+        M = int(rng.choice([1, 2, 7, 16, 17, 31, 33, 64, 65, 100, 129, 200, 257, 600]))
+        w = recipes.gaussian_weight(rows, cols, 500 + case)
+        ql = ts.QuantLinear(ts.quantize_tensor(w, **opts))
+        x = recipes.activations(M, cols, seed=case).cuda()
+        W = ql.dequantize_weight(torch.float32)
+        err = max_rel_err(ql(x).float(), x.float() @ W.T)
+        say("random", case, opts, rows, cols, M, err)
+        assert err <= TOL, (case, opts, rows, cols, M, err)
+
+
 def test_forward_group_fallbacks():
     """Mixed formats and M > 32 run one forward per layer."""
     ts = _ts()
