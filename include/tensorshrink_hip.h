@@ -102,6 +102,16 @@ const char* ts_version(void);
  * (rows x cols in the activation dtype) plus the GEMM library's workspace. */
 size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M);
 
+/* Bytes of device workspace (16-byte aligned) with which ts_qlinear_forward's
+ * fused prefill kernel splits K across workgroups for M activation rows: the
+ * splits' fp32 partial sums, k_split x M x rows x 4 bytes, k_split <= 8. Not 0
+ * only where the kernel's tiles would fill at most half of the compute units
+ * (few rows at small M, e.g. 4096 x 14336 at M = 256), and always below
+ * ts_forward_workspace_bytes(layer, M), so a workspace of this size never
+ * selects the GEMM library path. No counterpart in the reference (its Triton
+ * kernels do not split K). */
+size_t ts_forward_partials_bytes(const ts_qlayer* layer, int64_t M);
+
 /*
  * y[M, rows] = x[M, cols] @ W^T + outliers (+ bias), fp32 accumulation, stored
  * in y_dtype. Replaces fused_quantized_linear (triton_kernels.py:714-945) and,
@@ -111,7 +121,9 @@ size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M);
  * the layer into it and runs one hipBLASLt GEMM (bias in its epilogue);
  * otherwise the decode kernel on blocks of 16 tokens while that is the faster
  * kernel for the shape (M <= 32; <= 64 on layers of <= 8192 rows; <= 128 on
- * layers of <= 4096 rows), else the fused MFMA prefill kernel. x_dtype is TS_BF16 or TS_F16; bias
+ * layers of <= 4096 rows), else the fused MFMA prefill kernel (which splits K
+ * across workgroups when the workspace holds ts_forward_partials_bytes(layer,
+ * M) bytes and that size is not 0). x_dtype is TS_BF16 or TS_F16; bias
  * (may be NULL) has x_dtype. ldx/ldy are row strides in elements. Calls that
  * share a workspace must be ordered on one stream.
  */

@@ -59,6 +59,7 @@ PROTOTYPES = {
     "ts_status_str": (ctypes.c_char_p, [ctypes.c_int]),
     "ts_version": (ctypes.c_char_p, []),
     "ts_forward_workspace_bytes": (c_sz, [ctypes.POINTER(QLayer), c_i64]),
+    "ts_forward_partials_bytes": (c_sz, [ctypes.POINTER(QLayer), c_i64]),
     "ts_qlinear_forward": (ctypes.c_int, [ctypes.POINTER(QLayer), c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64,
                                           ctypes.c_int, c_vp, c_vp, c_sz, c_vp]),
     "ts_qlinear_forward_group": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(QLayer)), ctypes.c_int, c_vp, c_i64,

@@ -13,7 +13,8 @@ int decode_forward_group(const ts_qlayer* const* layers, int n, const uint16_t* 
                          int x_dtype, void* const* y, const int64_t* ldy, int y_dtype,
                          const uint16_t* const* bias, hipStream_t st);
 int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
-                    int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st);
+                    int64_t ldy, int y_dtype, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st);
+size_t prefill_partials_bytes(const ts_qlayer* L, int64_t M);
 int generic_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
                     int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st);
 int dequantize(const ts_qlayer* L, int mode, const int32_t* oidx, const uint16_t* oval, int64_t n_oidx,
@@ -109,6 +110,13 @@ size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M) {
   return ts::gemm_ws_bytes(layer);
 }
 
+size_t ts_forward_partials_bytes(const ts_qlayer* layer, int64_t M) {
+  if (!layer_ok(layer) || M <= 16 || ts::decode_mid_m(layer, M)) return 0;
+  const size_t b = ts::prefill_partials_bytes(layer, M);
+  // always below the library path's workspace, which takes precedence
+  return b < ts::gemm_ws_bytes(layer) ? b : 0;
+}
+
 int ts_qlinear_forward(const ts_qlayer* L, const void* x, int64_t M, int64_t ldx, int x_dtype, void* y, int64_t ldy,
                        int y_dtype, const void* bias, void* workspace, size_t workspace_bytes, void* stream) {
   if (!layer_ok(L) || !x || !y || M < 0) return TS_BAD_ARG;
@@ -135,7 +143,8 @@ int ts_qlinear_forward(const ts_qlayer* L, const void* x, int64_t M, int64_t ldx
         if (rc != TS_OK) break;
       }
     }
-    if (rc == TS_NOT_COVERED && M > 16) rc = ts::prefill_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
+    if (rc == TS_NOT_COVERED && M > 16)
+      rc = ts::prefill_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, workspace, workspace_bytes, S(stream));
   }
   if (rc == TS_NOT_COVERED) rc = ts::generic_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
   return rc;

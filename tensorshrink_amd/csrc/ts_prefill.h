@@ -81,6 +81,12 @@ struct PrefillArgs {
   int64_t cols;
   int64_t n_groups;
   int64_t m_tiles, n_tiles;
+  // K split across workgroups (k_split > 1): workgroup (tile, s) covers
+  // k-steps [s KT / k_split, (s + 1) KT / k_split) and stores its fp32 sums
+  // to part[s][M][N] (row stride N); splitk_reduce adds them up, with the
+  // bias, into y.
+  float* part;
+  int32_t k_split;
   // byte extents of the buffers read through buffer resources (all < 2^31)
   uint32_t x_bytes, p_bytes, meta_elems, dqm_bytes, s2_bytes, ocs_bytes;
 };
@@ -88,6 +94,9 @@ struct PrefillArgs {
 constexpr int PF_BM = 256;
 constexpr int PF_BK = 64;
 constexpr uint32_t PF_NO_COL = 0xffffu;  // column of the "no more outliers" entry
+constexpr int PF_CUS = 256;              // MI355X compute units
+constexpr int PF_SPLIT_MAX = 8;          // K splits per tile at most
+constexpr int PF_SPLIT_MIN_KT = 8;       // k-steps per split at least
 #ifndef PF_NW_WIDE
 #define PF_NW_WIDE 8  // waves per workgroup of the 256 x 256 tile
 #endif
@@ -172,7 +181,11 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   const int wm = wave & 1, wn = wave >> 1;  // wave (wm, wn) of the 2 x WN grid
   const uint32_t cb_lane = lane % CBC;
 
-  const int64_t tile = xcd_tile(blockIdx.x, a.m_tiles * a.n_tiles);
+  // the K splits of a tile are consecutive workgroup indices
+  const int P = a.k_split;
+  const int64_t lin = xcd_tile(blockIdx.x, a.m_tiles * a.n_tiles * P);
+  const int64_t tile = lin / P;
+  const int split = (int)(lin - tile * P);
   const int64_t mt = tile % a.m_tiles, nt = tile / a.m_tiles;
   const int64_t m0 = mt * BM, n0 = nt * BN;
 
@@ -194,7 +207,11 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   const uint32_t woff = (uint32_t)(wrow * a.pstride) + (wpart * CPT * SB) / 8;
   const uint32_t woff2 = RVQ ? (uint32_t)(wrow * a.s2stride) + (wpart * CPT) / 4 : 0u;
   const uint32_t gbase = (uint32_t)(wrow * a.n_groups) + (wpart * CPT) / GS;
-  const int KT = (int)(a.K / BK);
+  // this workgroup's k-steps: kt0 .. kt0 + KT - 1 (k-step indices below are
+  // relative to kt0)
+  const int KT_all = (int)(a.K / BK);
+  const int kt0 = (int)(((int64_t)split * KT_all) / P);
+  const int KT = (int)(((int64_t)(split + 1) * KT_all) / P) - kt0;
 
   // ---- raw load stage (registers only; nothing computes on the data here) --
   struct Stage {
@@ -213,7 +230,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   const uint32_t xstep = (uint32_t)((NT / 8) * a.ldx * 2);
   const int xcol = (tid & 7) * 8;
   auto load_x = [&](int kt, ts_u32x4* xr) {
-    kt = min(kt, KT - 1);
+    kt = kt0 + min(kt, KT - 1);
     const uint32_t kb = (uint32_t)kt * (BK * 2);
     const uint32_t oob = (kt * BK + xcol < a.cols) ? 0u : 0x80000000u;
 #pragma unroll
@@ -229,7 +246,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
       *reinterpret_cast<ts_u32x4*>(Ab + swz((tid >> 3) + (NT / 8) * i, tid & 7)) = xr[i];
   };
   auto load_stage = [&](int kt, Stage& S) {
-    kt = min(kt, KT - 1);  // a stage past the end re-reads the last k-step (never used)
+    kt = kt0 + min(kt, KT - 1);  // a stage past the end re-reads the last k-step (never used)
     const uint32_t off = woff + (uint32_t)kt * (BK * SB / 8);
     if constexpr (WB % 16 == 0) {
 #pragma unroll
@@ -390,7 +407,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
       en = ptr < oend ? tld : PF_NO_COL;
       en_stale = false;
     }
-    const uint32_t k0 = (uint32_t)kt * BK;
+    const uint32_t k0 = (uint32_t)(kt0 + kt) * BK;
     uint32_t* Bw = reinterpret_cast<uint32_t*>(Bs + buf * BN * BK);
     while ((e & 0xffffu) < k0 + BK) {  // rare: at most one row in 16 k-steps at 0.1 % outliers
       const int cc = (int)((e & 0xffffu) - k0);
@@ -428,8 +445,29 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   }
   if (a.has_out) {
     const int64_t r = min(n0 + wr, a.N);  // a row past N has an empty range
-    const uint32_t rb = (uint32_t)a.orow_ptr[r];
+    uint32_t rb = (uint32_t)a.orow_ptr[r];
     oend = (uint32_t)a.orow_ptr[min(r + 1, a.N)];
+    if (kt0 > 0) {
+      // a later K split starts at the row's first entry with column >=
+      // kt0 * BK: count the entries before it among the next 16 (one round
+      // trip), and search the rest of a longer row by bisection
+      const uint32_t kb = (uint32_t)kt0 * BK;
+      uint32_t below = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t v = oload(min(rb + j, oend > 0 ? oend - 1 : 0u));
+        below += (rb + j < oend && (v & 0xffffu) < kb) ? 1u : 0u;
+      }
+      rb += below;
+      if (below == 16) {
+        uint32_t hi = oend;
+        while (rb < hi) {
+          const uint32_t mid = rb + (hi - rb) / 2;
+          if ((a.ocs[mid] & 0xffffu) < kb) rb = mid + 1;
+          else hi = mid;
+        }
+      }
+    }
     e = rb < oend ? a.ocs[rb] : PF_NO_COL;
     ptr = rb + 1;
     tld = oload(min(ptr, oend > 0 ? oend - 1 : 0u));
@@ -580,7 +618,24 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   if (kt < KT) kstep(kt, S1, S0);
   }
 
-  // epilogue: bias, cast, store
+  // epilogue: bias, cast, store (a K split: its fp32 sums)
+  if (P > 1) {
+    float* pp = a.part + (int64_t)split * a.M * a.N;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t n = n0 + wn * (BN / WN) + 32 * j + (lane & 31);
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (m < a.M) pp[m * a.N + n] = acc[i][j][r];
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int64_t n = n0 + wn * (BN / WN) + 32 * j + (lane & 31);
@@ -617,29 +672,89 @@ inline int launch_prefill(PrefillArgs a, hipStream_t st) {
   if (!ts_set_smem_once(reinterpret_cast<const void*>(kern), smem, flags, ok)) return TS_HIP_ERROR;
   a.m_tiles = ts_cdiv(a.M, BM);
   a.n_tiles = ts_cdiv(a.N, BN);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(a.m_tiles * a.n_tiles)), dim3(64 * NW), smem, st, a);
+  if (a.k_split < 1 || a.k_split > a.K / PF_BK || (a.k_split > 1 && !a.part)) return TS_BAD_ARG;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(a.m_tiles * a.n_tiles * a.k_split)), dim3(64 * NW), smem, st, a);
   TS_CHECK_LAUNCH();
   return TS_OK;
 }
 
-// 256 x 256 tiles when they fill the CUs, else 256 x 128, or 128 x 128 when
-// those would still leave CUs idle and 128 x 128 tiles fit one round.
+// Launch shape of the prefill kernel for an M x N x K product of a layer
+// with `bits`-bit codes (cb: with a codebook). Tiles: 256 x 256 on 8 waves
+// when they fill the CUs, else 256 x 128 on 4 waves, or 128 x 128 when 256 x
+// 128 tiles would still leave CUs idle and 128 x 128 tiles fit one round.
+// K is split across k_split (1-8) workgroups per tile, at least 8 k-steps
+// each, where that is estimated faster: few tiles (narrow layers or few rows
+// at small M: 4096 x 14336 at M = 256 has 64 tiles for 256 CUs) or a partial
+// last round of deep tiles. Estimate, from MI355X measurements: workgroups
+// per CU (rounded up) x k-steps per split x the tile's k-step time (1.25 us
+// for 128 x 128, 1.75 for 256 x 128, 2.9 for 256 x 256), where two 128 x 128
+// workgroups whose LDS fits one CU together share it at 1.5x the time of
+// one; plus, with splits, the fp32 partial sums' HBM traffic (k_split * M *
+// N * 4 bytes written and read, at 4 TB/s) and 2 us for the reduction
+// launch. A split must win by 3 %. The partials stay below the GEMM library
+// path's workspace (rows x cols x 2 + 32 MB).
+struct PrefillPlan {
+  int bm, bn;
+  int64_t tiles;
+  int splits;
+};
+inline PrefillPlan prefill_plan(int64_t M, int64_t N, int64_t K, int bits, bool cb) {
+  PrefillPlan p{};
+  if (ts_cdiv(M, PF_BM) * ts_cdiv(N, 256) >= PF_CUS) {
+    p.bm = 256; p.bn = 256;
+  } else if (ts_cdiv(M, PF_BM) * ts_cdiv(N, 128) < PF_CUS && ts_cdiv(M, 128) * ts_cdiv(N, 128) <= PF_CUS) {
+    p.bm = 128; p.bn = 128;
+  } else {
+    p.bm = 256; p.bn = 128;
+  }
+  p.tiles = ts_cdiv(M, p.bm) * ts_cdiv(N, p.bn);
+  p.splits = 1;
+  // (the LDS size of prefill_smem<bits, cb, 128, 128>; registers allow two
+  // such workgroups per CU, but not two of the larger tiles)
+  const size_t lds128 = (size_t)2 * 256 * PF_BK * 2 + (cb ? ((size_t)1 << bits) * 32 * 4 : 0);
+  const bool pair = p.bm == 128 && 2 * lds128 <= 160 * 1024;
+  const double tk = p.bn == 256 ? 2.9 : (p.bm == 256 ? 1.75 : 1.25);
+  const int64_t KT = K / PF_BK;
+  const double cap = (double)N * (double)K * 2 + (double)(32 << 20);
+  double best = 0;
+  for (int s = 1; s <= PF_SPLIT_MAX; ++s) {
+    if (s > 1 && (KT / s < PF_SPLIT_MIN_KT || (double)s * M * N * 4 >= cap)) break;
+    const int64_t wpc = ts_cdiv(p.tiles * s, PF_CUS);
+    const double rounds = pair ? (double)(wpc / 2) * 1.5 + (double)(wpc % 2) : (double)wpc;
+    double t = rounds * (double)ts_cdiv(KT, s) * tk;
+    if (s > 1) t += ((double)s * M * N * 8 + (double)M * N * 2) * 1e6 / 4e12 + 2.0;
+    if (s == 1 || t < 0.97 * best) {
+      best = t;
+      p.splits = s;
+    }
+  }
+  return p;
+}
+inline size_t prefill_part_bytes(const PrefillPlan& p, int64_t M, int64_t N) {
+  return p.splits > 1 ? (size_t)p.splits * (size_t)M * (size_t)N * 4 : 0;
+}
+
+// y = sum of the K splits' fp32 sums (+ bias), cast to y's dtype.
+int launch_splitk_reduce(const PrefillArgs& a, bool bf16, hipStream_t st);
+
+// a.part / a.k_split: set by the caller (k_split = 1 without workspace)
 template <int BITS, int GS, bool BF16, bool CB, bool RVQ>
 inline int launch_prefill_tiles(PrefillArgs& a, hipStream_t st) {
   const bool dq = a.dqsc != nullptr;
-  const bool wide = ts_cdiv(a.M, PF_BM) * ts_cdiv(a.N, 256) >= 256;
-  if (wide) {
-    return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 256, PF_NW_WIDE>(a, st)
-              : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 256, PF_NW_WIDE>(a, st);
-  }
-  // 128-row tiles when they still fit one round of workgroups: twice the
-  // workgroups of 256-row tiles (or half their padding at M <= 128)
-  if (ts_cdiv(a.M, PF_BM) * ts_cdiv(a.N, 128) < 256 && ts_cdiv(a.M, 128) * ts_cdiv(a.N, 128) <= 256) {
-    return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, 4, 128>(a, st)
-              : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128, 4, 128>(a, st);
-  }
-  return dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, 4>(a, st)
+  const PrefillPlan p = prefill_plan(a.M, a.N, a.K, BITS, CB);
+  int rc;
+  if (p.bn == 256) {
+    rc = dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 256, PF_NW_WIDE>(a, st)
+            : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 256, PF_NW_WIDE>(a, st);
+  } else if (p.bm == 128) {
+    rc = dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, 4, 128>(a, st)
+            : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128, 4, 128>(a, st);
+  } else {
+    rc = dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, 4>(a, st)
             : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128, 4>(a, st);
+  }
+  if (rc == TS_OK && a.k_split > 1) rc = launch_splitk_reduce(a, BF16, st);
+  return rc;
 }
 
 // Per-(bit width, group size) launchers, one translation unit each

@@ -4,8 +4,66 @@
 
 namespace ts {
 
+// y[m][n] = cast(sum_s part[s][m][n] + bias[n]); four outputs of a row per
+// thread when N % 4 == 0 (16-byte partial reads), else one.
+template <bool BF16, bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int P, int64_t M,
+                                                            int64_t N, const uint16_t* __restrict__ bias, void* y,
+                                                            int64_t ldy, int y_dtype) {
+  constexpr int V = VEC ? 4 : 1;
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float v[V];
+  if constexpr (VEC) {
+    float4 t = *reinterpret_cast<const float4*>(part + i);
+    for (int s = 1; s < P; ++s) {
+      const float4 u = *reinterpret_cast<const float4*>(part + (int64_t)s * M * N + i);
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  } else {
+    float t = part[i];
+    for (int s = 1; s < P; ++s) t += part[(int64_t)s * M * N + i];
+    v[0] = t;
+  }
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    if (bias) v[j] += XT<BF16>::to_f(bias[n + j]);
+    const int64_t off = m * ldy + n + j;
+    if (y_dtype == TS_F32) reinterpret_cast<float*>(y)[off] = v[j];
+    else reinterpret_cast<uint16_t*>(y)[off] = XT<BF16>::from_f(v[j]);
+  }
+}
+
+int launch_splitk_reduce(const PrefillArgs& a, bool bf16, hipStream_t st) {
+  const bool vec = a.N % 4 == 0;
+  const int64_t threads = vec ? a.M * a.N / 4 : a.M * a.N;
+  const dim3 grid((unsigned)ts_cdiv(threads, 256)), block(256);
+  const uint16_t* b = a.bias;
+  if (bf16) {
+    if (vec) hipLaunchKernelGGL((splitk_reduce_kernel<true, true>), grid, block, 0, st, a.part, a.k_split, a.M, a.N, b, a.y, a.ldy, a.y_dtype);
+    else hipLaunchKernelGGL((splitk_reduce_kernel<true, false>), grid, block, 0, st, a.part, a.k_split, a.M, a.N, b, a.y, a.ldy, a.y_dtype);
+  } else {
+    if (vec) hipLaunchKernelGGL((splitk_reduce_kernel<false, true>), grid, block, 0, st, a.part, a.k_split, a.M, a.N, b, a.y, a.ldy, a.y_dtype);
+    else hipLaunchKernelGGL((splitk_reduce_kernel<false, false>), grid, block, 0, st, a.part, a.k_split, a.M, a.N, b, a.y, a.ldy, a.y_dtype);
+  }
+  TS_CHECK_LAUNCH();
+  return TS_OK;
+}
+
+// The launchers' (bits, codebook) template arguments for a layer: 6-bit
+// (RVQ) layers run the 4-bit kernel without a codebook.
+static int prefill_bits(const ts_qlayer* L) { return L->bits == 6 ? 4 : L->bits; }
+static bool prefill_codebook(const ts_qlayer* L) { return L->bits != 6 && L->codebook != nullptr; }
+
+size_t prefill_partials_bytes(const ts_qlayer* L, int64_t M) {
+  if (M <= 16 || L->padded_cols % PF_BK != 0) return 0;
+  return prefill_part_bytes(prefill_plan(M, L->rows, L->padded_cols, prefill_bits(L), prefill_codebook(L)), M, L->rows);
+}
+
 int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
-                    int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st) {
+                    int64_t ldy, int y_dtype, const uint16_t* bias, void* ws, size_t ws_bytes, hipStream_t st) {
   if (L->padded_cols % PF_BK != 0) return TS_NOT_COVERED;
   const bool has_out = L->n_outliers > 0;
   // Outliers are walked per row in column order with 16-bit columns; the walk
@@ -64,6 +122,15 @@ int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ld
   a.meta_elems = (uint32_t)meta;
   a.dqm_bytes = (uint32_t)dqm;
   a.s2_bytes = (uint32_t)s2;
+  // K split when the plan asks for one and the workspace holds the partials
+  const PrefillPlan plan = prefill_plan(M, L->rows, L->padded_cols, prefill_bits(L), prefill_codebook(L));
+  const size_t pb = prefill_part_bytes(plan, M, L->rows);
+  a.k_split = 1;
+  a.part = nullptr;
+  if (pb > 0 && ws && ws_bytes >= pb && (reinterpret_cast<uintptr_t>(ws) & 15) == 0) {
+    a.k_split = plan.splits;
+    a.part = static_cast<float*>(ws);
+  }
   const bool bf16 = x_dtype == TS_BF16;
   switch (L->bits * 1000 + L->group_size) {
     case 2064: return prefill_b2_g64(L, a, bf16, st);

@@ -377,13 +377,17 @@ class QuantLinear(nn.Module):
         b = self._bias_as(in_dtype)
         dt = L.dtype_code(in_dtype)
         lib = L.load()
-        # no workspace: the decode kernel (M <= 16, and blocks of 16 tokens
-        # up to 32-128 rows by layer height), else the fused dequant-into-LDS
-        # MFMA kernel
+        # the decode kernel (M <= 16, and blocks of 16 tokens up to 32-128
+        # rows by layer height), else the fused dequant-into-LDS MFMA kernel;
+        # its fp32 K-split partial sums, where the shape uses them, in a
+        # workspace from torch's caching allocator (never the GEMM library
+        # path's size)
+        nws = lib.ts_forward_partials_bytes(ctypes.byref(self._layer), M) if M > 16 else 0
+        ws = torch.empty(nws, dtype=torch.uint8, device=x.device) if nws else None
         with torch.cuda.device(x.device):
             L.check(lib.ts_qlinear_forward(ctypes.byref(self._layer), x2d.data_ptr(), M, self.in_features, dt,
-                                           y.data_ptr(), self.out_features, dt, L.ptr(b), None, 0,
-                                           L.stream_ptr(x.device)), "qlinear forward")
+                                           y.data_ptr(), self.out_features, dt, L.ptr(b),
+                                           L.ptr(ws), nws, L.stream_ptr(x.device)), "qlinear forward")
         return y.reshape(*lead, self.out_features)
 
     @staticmethod

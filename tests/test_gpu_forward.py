@@ -379,6 +379,74 @@ def test_forward_random_shapes():
         assert err <= TOL, (case, opts, rows, cols, M, err)
 
 
+def _dense_row_weight(rows, cols, seed):
+    """Gaussian weight with two rows of large values (row 5 on every column,
+    row 77 on every third), so the top-k outliers crowd those rows and every
+    other row holds dozens: K splits then start past 16 of a row's entries."""
+    w = recipes.gaussian_weight(rows, cols, seed)
+    w[5, :] *= 50
+    w[77, ::3] *= 50
+    return w
+
+
+@pytest.mark.parametrize("fmt,rows,cols,M,xdt,bias", [
+    (dict(bits=4, group_size=128, double_quant=True, nf_quant=True), 1024, 4096, 200, torch.bfloat16, True),
+    (dict(bits=8, group_size=128, double_quant=True, nf_quant=True), 4096, 2048, 300, torch.bfloat16, False),
+    (dict(bits=6, group_size=128, double_quant=True), 512, 8192, 160, torch.bfloat16, True),
+    (dict(bits=2, group_size=64, double_quant=True), 1002, 2048, 140, torch.float16, True),
+    (dict(bits=4, group_size=64), 1024, 4096, 2048, torch.float16, False),
+])
+def test_forward_split_k(fmt, rows, cols, M, xdt, bias):
+    """Layers whose prefill tiles fill at most half of the CUs: QuantLinear
+    hands the fused kernel a workspace for K-split partial sums; the split
+    result (with dense outlier rows, bias, fp16 / bf16) meets the float64
+    product and agrees with the unsplit kernel."""
+    ts = _ts()
+    from tensorshrink_amd import _lib as L
+    w = _dense_row_weight(rows, cols, 900 + rows)
+    b = (torch.randn(rows, generator=torch.Generator().manual_seed(7)) * 0.5).to(xdt) if bias else None
+    ql = ts.QuantLinear(ts.quantize_tensor(w, outlier_frac=0.01, **fmt), b)
+    lay = ctypes.byref(ql._layer)
+    nws = L.load().ts_forward_partials_bytes(lay, M)
+    assert nws > 0 and nws % (4 * M * rows) == 0 and nws < L.load().ts_forward_workspace_bytes(lay, M)
+    x = recipes.activations(M, cols, seed=M, dtype=xdt).cuda()
+    W = ql.dequantize_weight(torch.float32).double()
+    y_ref = x.double() @ W.T
+    if b is not None:
+        y_ref += b.double().cuda()
+    y = ql(x)
+    y0 = _forward_no_workspace(ql, x)
+    say("split-k", fmt, rows, cols, M, nws // (4 * M * rows), max_rel_err(y, y_ref), max_rel_err(y, y0))
+    assert y.dtype == xdt
+    assert max_rel_err(y, y_ref) <= TOL
+    assert max_rel_err(y0, y_ref) <= TOL
+    assert max_rel_err(y, y0) <= 4e-3
+
+
+def test_forward_split_k_f32_strided():
+    """The K-split path through the C-ABI: fp32 output with a row stride past
+    the layer's rows (the stride tail stays untouched), two calls in a row
+    sharing one workspace, the second with fewer rows."""
+    ts = _ts()
+    from tensorshrink_amd import _lib as L
+    rows, cols, ldy = 1024, 4096, 1100
+    ql = ts.QuantLinear(ts.quantize_tensor(_dense_row_weight(rows, cols, 31), **dict(NF4, outlier_frac=0.01)))
+    W = ql.dequantize_weight(torch.float32).double()
+    lib, lay = L.load(), ctypes.byref(ql._layer)
+    ws = torch.empty(lib.ts_forward_partials_bytes(lay, 300), dtype=torch.uint8, device="cuda")
+    for M in (300, 150):
+        need = lib.ts_forward_partials_bytes(lay, M)
+        assert 0 < need <= ws.numel()
+        x = recipes.activations(M, cols, seed=M).cuda()
+        y = torch.full((M, ldy), 7.0, dtype=torch.float32, device="cuda")
+        L.check(lib.ts_qlinear_forward(lay, x.data_ptr(), M, cols, L.dtype_code(x.dtype), y.data_ptr(), ldy,
+                                       L.dtype_code(torch.float32), None, ws.data_ptr(), ws.numel(),
+                                       L.stream_ptr()), "split fwd")
+        y_ref = x.double() @ W.T
+        assert max_rel_err(y[:, :rows], y_ref) <= TOL
+        assert bool((y[:, rows:] == 7.0).all())
+
+
 def test_forward_group_fallbacks():
     """Mixed formats and M > 32 run one forward per layer."""
     ts = _ts()

@@ -185,3 +185,49 @@ def test_forward_workspace_bytes():
     assert lib.ts_forward_workspace_bytes(ctypes.byref(q), 2048) == need
     q.n_groups = 31  # inconsistent view
     assert lib.ts_forward_workspace_bytes(ctypes.byref(q), 2048) == 0
+
+
+def test_forward_partials_bytes():
+    """Host-only sizing of the fused prefill kernel's K-split workspace,
+    k_split x M x rows x 4 bytes: 0 at decode sizes, where the tiles fill the
+    CUs and where K is too short to split; the split counts the launch plan
+    picks for few tiles (two 4-wave 128 x 128 workgroups share a CU when their
+    LDS fits, which NF8's 256-entry codebook copies prevent); always below
+    the GEMM path's workspace. No GPU call."""
+    import ctypes
+    L, lib = _lib()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced by the sizing call
+
+    def layer(rows, cols, bits=4, codebook=False):
+        q = L.QLayer()
+        q.bits, q.group_size, q.rows, q.cols = bits, 128, rows, cols
+        q.padded_cols, q.n_groups = cols, cols // 128
+        q.packed = q.scale = q.gmin = fake
+        if codebook:
+            q.codebook = fake
+        q.packed_stride = cols * bits // 8
+        return q
+
+    def splits(rows, cols, M, **kw):
+        n = lib.ts_forward_partials_bytes(ctypes.byref(layer(rows, cols, **kw)), M)
+        assert n % (4 * M * rows) == 0
+        k = n // (4 * M * rows)
+        if n:
+            assert 2 <= k <= 8
+            assert n < lib.ts_forward_workspace_bytes(ctypes.byref(layer(rows, cols, **kw)), M)
+        return k
+
+    # down projection at M = 256: 64 tiles of 128 x 128
+    assert splits(4096, 14336, 256) == 8
+    assert splits(4096, 14336, 256, bits=8, codebook=True) == 4
+    # k / v at M = 2048: 128 tiles
+    assert splits(1024, 4096, 2048) == 4
+    # 512 x 8192 at M = 160: 8 tiles, 128 k-steps
+    assert splits(512, 8192, 160) == 8
+    # tiles filling the CUs: 14336 x 4096 at M = 2048 (448 tiles of 256 x 256)
+    assert splits(14336, 4096, 2048) == 0
+    # decode sizes, and the mid-M decode range (4096 rows = 256 row tiles)
+    for M in (1, 16, 17, 64, 128):
+        assert splits(4096, 4096, M) == 0
+    # too few k-steps to split (256 columns = 4 k-steps)
+    assert splits(4096, 256, 300) == 0
