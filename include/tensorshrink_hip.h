@@ -105,8 +105,9 @@ size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M);
 /* Bytes of device workspace (16-byte aligned) with which ts_qlinear_forward's
  * fused prefill kernel splits K across workgroups for M activation rows: the
  * splits' fp32 partial sums, k_split x M x rows x 4 bytes, k_split <= 8. Not 0
- * only where the kernel's tiles would fill at most half of the compute units
- * (few rows at small M, e.g. 4096 x 14336 at M = 256), and always below
+ * only where the launch plan estimates a split faster: tiles that would leave
+ * compute units idle (few rows or small M, e.g. 4096 x 14336 at M = 256) or a
+ * partial last round of deep tiles. 0 where the decode kernel runs. Always below
  * ts_forward_workspace_bytes(layer, M), so a workspace of this size never
  * selects the GEMM library path. No counterpart in the reference (its Triton
  * kernels do not split K). */
@@ -119,11 +120,13 @@ size_t ts_forward_partials_bytes(const ts_qlayer* layer, int64_t M);
  * (modules.py:896-922): M <= 16 runs the HBM-bound decode kernel; M > 16
  * with a workspace of ts_forward_workspace_bytes(layer, M) bytes dequantizes
  * the layer into it and runs one hipBLASLt GEMM (bias in its epilogue);
- * otherwise the decode kernel on blocks of 16 tokens while that is the faster
- * kernel for the shape (M <= 32; <= 64 on layers of <= 8192 rows; <= 128 on
- * layers of <= 4096 rows), else the fused MFMA prefill kernel (which splits K
- * across workgroups when the workspace holds ts_forward_partials_bytes(layer,
- * M) bytes and that size is not 0). x_dtype is TS_BF16 or TS_F16; bias
+ * otherwise the decode kernel on blocks of 16 tokens where that is the faster
+ * kernel for the shape (M <= 32, or <= 24 when cols > 8192, on layers of at
+ * most 4096 rows with codes of at most 6 bits), else the fused MFMA prefill
+ * kernel, which splits K across workgroups when the workspace holds
+ * ts_forward_partials_bytes(layer, M) bytes and that size is not 0 (layers
+ * the prefill kernel does not take: the decode kernel in passes of 64 rows,
+ * else a one-thread-per-output kernel). x_dtype is TS_BF16 or TS_F16; bias
  * (may be NULL) has x_dtype. ldx/ldy are row strides in elements. Calls that
  * share a workspace must be ordered on one stream.
  */
@@ -133,9 +136,11 @@ int ts_qlinear_forward(const ts_qlayer* layer, const void* x, int64_t M, int64_t
 
 /*
  * The forward above for n (1..4) layers that read the same x (q/k/v, gate/up)
- * in one launch: y[l][M, rows_l] = x @ W_l^T (+ bias[l]). Covers M <= 32 with
- * layers of one format (bits, group size, cols, codebook / double-quant /
- * stage-2 kind); returns TS_NOT_COVERED otherwise, and the caller runs
+ * in one launch: y[l][M, rows_l] = x @ W_l^T (+ bias[l]). Covers M <= 16, and
+ * M <= 32 when the layers have at most 12288 rows in all (q/k/v; not the
+ * taller gate/up, where per-layer prefill launches win), with layers of one
+ * format (bits, group size, cols, codebook / double-quant / stage-2 kind);
+ * returns TS_NOT_COVERED otherwise, and the caller runs
  * ts_qlinear_forward per layer. No counterpart in the reference, which calls
  * fused_quantized_linear once per QuantLinear (modules.py:896-905); this
  * replaces that sequence of calls for layers sharing an input. bias may be

@@ -27,19 +27,26 @@ int gemm_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, 
 // reference switches to dequantize + F.linear above 64 rows; measured here the
 // GEMM path is faster than the fused MFMA kernel from 17 rows on).
 constexpr int64_t GEMM_MIN_M = 17;
-// Up to DEC_M_MAX rows of x the decode kernel runs them as blocks of 16
-// tokens that share each code-table read (the reference's fused kernel covers
-// M <= 64, modules.py:881-894). Above 16 rows it competes with the fused MFMA
-// prefill kernel, whose 256-row tiles leave most CUs idle at small M on
-// layers of few rows; measured on MI355X (4-bit, K = 4096 / 14336): decode
-// wins up to 32 rows on every shape, up to 64 rows on layers of at most 512
-// 16-row tiles, and up to 128 rows (two passes of 64) on layers of at most 256
-// tiles.
+// Up to DEC_M_MAX rows of x per launch the decode kernel runs them as blocks
+// of 16 tokens that share each code-table read (the reference's fused kernel
+// covers M <= 64, modules.py:881-894). Above 16 rows it competes with the
+// fused MFMA prefill kernel, which splits K where its tiles would leave CUs
+// idle. Measured on MI355X (NF4 / NF8 / 2-bit / 6-bit RVQ layers of 1024-28672
+// rows, K = 4096-28672): decode wins up to 32 rows (24 when K > 8192) on
+// layers of at most 256 16-row tiles with codes of at most 6 bits; 8-bit
+// layers (by at most 3 us at 17-24 rows on the smallest ones) and taller
+// layers run the prefill kernel from 17 rows.
 constexpr int64_t DEC_M_MAX = 64;
 inline bool decode_mid_m(const ts_qlayer* L, int64_t M) {
-  const int64_t tiles = ts_cdiv(L->rows, 16);
-  return M <= 32 || (M <= 64 && tiles <= 512) || (M <= 2 * DEC_M_MAX && tiles <= 256);
+  if (M <= 16) return true;
+  return L->bits != 8 && ts_cdiv(L->rows, 16) <= 256 && M <= (L->cols > 8192 ? 24 : 32);
 }
+// Grouped decode launches (q/k/v, gate/up) above 16 rows: up to 32 rows while
+// the group has at most this many 16-row tiles in all. Measured: q/k/v of a
+// 4096-wide model (384 tiles) in one decode launch takes 26-52 us at 17-32
+// rows against 60-73 us for three prefill launches (2-bit to NF8); gate/up
+// (1792 tiles) loses to two prefill launches from 24 rows (17 at 8 and 2 bits).
+constexpr int64_t DEC_GROUP_TILES_MAX = 768;
 int outlier_row_ptr(const int32_t* row, int64_t n, int64_t rows, int32_t* row_ptr, hipStream_t st);
 int tile_outlier_max(const int32_t* rp, int64_t rows, int32_t* out, hipStream_t st);
 int build_tile_outliers(const int32_t* rp, const int32_t* orow, const int32_t* ocol, const uint16_t* odelta,
@@ -111,7 +118,7 @@ size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M) {
 }
 
 size_t ts_forward_partials_bytes(const ts_qlayer* layer, int64_t M) {
-  if (!layer_ok(layer) || M <= 16 || ts::decode_mid_m(layer, M)) return 0;
+  if (!layer_ok(layer) || ts::decode_mid_m(layer, M)) return 0;
   const size_t b = ts::prefill_partials_bytes(layer, M);
   // always below the library path's workspace, which takes precedence
   return b < ts::gemm_ws_bytes(layer) ? b : 0;
@@ -133,18 +140,26 @@ int ts_qlinear_forward(const ts_qlayer* L, const void* x, int64_t M, int64_t ldx
   if (M >= ts::GEMM_MIN_M && workspace)
     rc = ts::gemm_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, workspace, workspace_bytes, S(stream));
   if (rc == TS_NOT_COVERED && aligned) {
-    if (M <= 16 || ts::decode_mid_m(L, M)) {
-      // passes of at most DEC_M_MAX rows; the first pass decides coverage
-      // (the format checks run before any launch)
+    // the decode kernel in passes of at most DEC_M_MAX rows; the first pass
+    // decides coverage (the format checks run before any launch)
+    auto decode_passes = [&]() {
       const size_t ybytes = y_dtype == TS_F32 ? 4 : 2;
+      int r = TS_NOT_COVERED;
       for (int64_t m0 = 0; m0 < M; m0 += ts::DEC_M_MAX) {
-        rc = ts::decode_forward(L, xp + m0 * ldx, std::min(ts::DEC_M_MAX, M - m0), ldx, x_dtype,
-                                static_cast<char*>(y) + m0 * ldy * ybytes, ldy, y_dtype, bp, S(stream));
-        if (rc != TS_OK) break;
+        r = ts::decode_forward(L, xp + m0 * ldx, std::min(ts::DEC_M_MAX, M - m0), ldx, x_dtype,
+                               static_cast<char*>(y) + m0 * ldy * ybytes, ldy, y_dtype, bp, S(stream));
+        if (r != TS_OK) break;
       }
-    }
+      return r;
+    };
+    const bool dec = ts::decode_mid_m(L, M);
+    if (dec) rc = decode_passes();
     if (rc == TS_NOT_COVERED && M > 16)
       rc = ts::prefill_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, workspace, workspace_bytes, S(stream));
+    // layers the prefill kernel does not take (group sizes below 64 with
+    // columns not a multiple of 64, columns past its 16-bit outlier walk):
+    // the decode kernel's token blocks before the one-thread-per-output kernel
+    if (rc == TS_NOT_COVERED && !dec) rc = decode_passes();
   }
   if (rc == TS_NOT_COVERED) rc = ts::generic_forward(L, xp, M, ldx, x_dtype, y, ldy, y_dtype, bp, S(stream));
   return rc;
@@ -164,7 +179,12 @@ int ts_qlinear_forward_group(const ts_qlayer* const* layers, int n_layers, const
   if (M == 0) return TS_OK;
   const ts_qlayer* L0 = layers[0];
   const bool aligned = (L0->cols % 8 == 0) && (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
-  if (!aligned || M > 32) return TS_NOT_COVERED;  // (decode wins up to 32 rows on every shape)
+  if (!aligned || M > 32) return TS_NOT_COVERED;
+  if (M > 16) {
+    int64_t tiles = 0;
+    for (int l = 0; l < n_layers; ++l) tiles += ts_cdiv(layers[l]->rows, 16);
+    if (tiles > ts::DEC_GROUP_TILES_MAX) return TS_NOT_COVERED;
+  }
   return ts::decode_forward_group(layers, n_layers, static_cast<const uint16_t*>(x), M, ldx, x_dtype, y, ldy, y_dtype,
                                   reinterpret_cast<const uint16_t* const*>(bias), S(stream));
 }

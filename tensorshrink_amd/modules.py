@@ -377,8 +377,9 @@ class QuantLinear(nn.Module):
         b = self._bias_as(in_dtype)
         dt = L.dtype_code(in_dtype)
         lib = L.load()
-        # the decode kernel (M <= 16, and blocks of 16 tokens up to 32-128
-        # rows by layer height), else the fused dequant-into-LDS MFMA kernel;
+        # the decode kernel (M <= 16, and blocks of 16 tokens up to 24-32 rows
+        # on layers of at most 4096 rows and 6-bit codes), else the fused
+        # dequant-into-LDS MFMA kernel;
         # its fp32 K-split partial sums, where the shape uses them, in a
         # workspace from torch's caching allocator (never the GEMM library
         # path's size)
@@ -393,10 +394,11 @@ class QuantLinear(nn.Module):
     @staticmethod
     def forward_group(layers: Sequence["QuantLinear"], x: torch.Tensor) -> List[torch.Tensor]:
         """[layer(x) for layer in layers] in one kernel launch when the layers
-        share a format and the input has at most 32 rows (q/k/v or gate/up at
-        decode); otherwise, or when the launch is not covered, one forward per
-        layer. No counterpart in the reference, whose model code calls each
-        QuantLinear in turn (modules.py:896-905)."""
+        share a format and the input has at most 16 rows, or at most 32 with
+        at most 12288 weight rows in all (q/k/v or gate/up at decode; q/k/v
+        at short prefills); otherwise, or when the launch is not covered, one
+        forward per layer. No counterpart in the reference, whose model code
+        calls each QuantLinear in turn (modules.py:896-905)."""
         layers = list(layers)
         in_dtype = x.dtype
         M = 1
