@@ -226,8 +226,15 @@ def test_forward_partials_bytes():
     assert splits(512, 8192, 160) == 8
     # tiles filling the CUs: 14336 x 4096 at M = 2048 (448 tiles of 256 x 256)
     assert splits(14336, 4096, 2048) == 0
-    # decode sizes, and the mid-M decode range (4096 rows = 256 row tiles)
-    for M in (1, 16, 17, 64, 128):
+    # decode sizes: up to 16 rows, and up to 32 (24 for K > 8192) on layers
+    # of at most 256 row tiles with codes of at most 6 bits
+    for M in (1, 16, 17, 32):
         assert splits(4096, 4096, M) == 0
+    assert splits(4096, 14336, 24) == 0
+    assert splits(4096, 14336, 25) > 0
+    assert splits(4096, 4096, 33) > 0
+    # 8-bit layers and taller layers take the prefill kernel from 17 rows
+    assert splits(4096, 4096, 17, bits=8, codebook=True) > 0
+    assert splits(8192, 4096, 17) > 0
     # too few k-steps to split (256 columns = 4 k-steps)
     assert splits(4096, 256, 300) == 0
