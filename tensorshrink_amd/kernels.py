@@ -146,8 +146,11 @@ def fused_quantized_linear(
     if out is None or out.shape != (M, out_features) or out.dtype != ydt or not out.is_contiguous():
         out = torch.empty(M, out_features, dtype=ydt, device=x.device)
     b = bias.to(compute_dtype).contiguous() if bias is not None else None
+    # the prefill kernel's K-split partial sums, where the shape uses them
+    nws = lib.ts_forward_partials_bytes(ctypes.byref(s), M) if M > 16 else 0
+    ws = torch.empty(nws, dtype=torch.uint8, device=x.device) if nws else None
     rc = lib.ts_qlinear_forward(ctypes.byref(s), x2d.data_ptr(), M, x2d.shape[1], L.dtype_code(compute_dtype),
-                                out.data_ptr(), out_features, L.dtype_code(ydt), L.ptr(b), None, 0,
+                                out.data_ptr(), out_features, L.dtype_code(ydt), L.ptr(b), L.ptr(ws), nws,
                                 L.stream_ptr(x.device))
     if rc == L.TS_NOT_COVERED:
         return None
