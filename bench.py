@@ -34,7 +34,10 @@ Alongside it (extra keys of the same JSON line):
                        and 6-bit RVQ, 2*M*N*K flops / GPU time vs 2.5 PFLOP/s,
                        through QuantLinear.forward (the fused dequant-into-LDS
                        MFMA kernel), with dequantize + hipBLASLt GEMM beside it
-                       as "library_reference";
+                       as "library_reference"; "short_prompt": M=256 through
+                       config 3's seven 4-bit linears (the fused kernel
+                       splitting K where few tiles) beside the same library
+                       reference;
   * "quantize"       - BASELINE config 5's GPU GOAP quantize (28672x8192) through
                        the public API, wall time, with the oracle CPU codec timed
                        on the same full weight;
@@ -361,6 +364,33 @@ def _forward_gemm(q, x):
 _WS: dict = {}
 
 
+def _timed_linears(lins, xs, M, fwd, steps):
+    """Per-linear GPU time (HIP events, one round of warmup absorbed) of
+    fwd(q, x) over `steps` rounds of the linears; TFLOPS over all of them."""
+    flops = {name: 2.0 * M * q.out_features * q.in_features for name, q in lins}
+    for _, q in lins:
+        fwd(q, xs[q.in_features])
+    torch.cuda.synchronize()
+    times = {name: [] for name, _ in lins}
+    evs = []
+    for s in range(steps):
+        for name, q in lins:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fwd(q, xs[q.in_features])
+            e1.record()
+            evs.append((name, e0, e1))
+    torch.cuda.synchronize()
+    for name, e0, e1 in evs[len(lins):]:  # the first round absorbs the empty-queue start
+        times[name].append(e0.elapsed_time(e1))
+    tot_f = sum(flops[n] * len(times[n]) for n in times)
+    tot_ms = sum(sum(times[n]) for n in times)
+    tflops = tot_f / (tot_ms * 1e-3) / 1e12
+    return {"tflops": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+            "per_linear_us": {n: round(sum(t) / len(t) * 1e3, 1) for n, t in times.items()},
+            "layer_us": round(sum(sum(t) / len(t) for t in times.values()) * 1e3, 1)}
+
+
 def bench_prefill(args):
     import recipes
     import tensorshrink_amd as ts
@@ -374,29 +404,11 @@ def bench_prefill(args):
             lins.append((name, ts.QuantLinear(ts.quantize_tensor(w, **opts))))
             del w
         xs = {4096: recipes.activations(M, 4096).cuda(), 14336: recipes.activations(M, 14336).cuda()}
-        flops = {name: 2.0 * M * q.out_features * q.in_features for name, q in lins}
 
         def timed(fwd):
-            for _, q in lins:
-                fwd(q, xs[q.in_features])
-            torch.cuda.synchronize()
-            times = {name: [] for name, _ in lins}
-            evs = []
-            for s in range(args.prefill_steps):
-                for name, q in lins:
-                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    e0.record()
-                    fwd(q, xs[q.in_features])
-                    e1.record()
-                    evs.append((name, e0, e1))
-            torch.cuda.synchronize()
-            for name, e0, e1 in evs[len(lins):]:  # the first round absorbs the empty-queue start
-                times[name].append(e0.elapsed_time(e1))
-            tot_f = sum(flops[n] * len(times[n]) for n in times)
-            tot_ms = sum(sum(times[n]) for n in times)
-            tflops = tot_f / (tot_ms * 1e-3) / 1e12
-            return {"tflops": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                    "per_linear_us": {n: round(sum(t) / len(t) * 1e3, 1) for n, t in times.items()}}
+            r = _timed_linears(lins, xs, M, fwd, args.prefill_steps)
+            r.pop("layer_us")
+            return r
 
         r = timed(lambda q, x: q(x))
         r["path"] = ("QuantLinear.forward: the fused dequant-into-LDS MFMA kernel (ts::prefill_kernel, "
@@ -409,6 +421,33 @@ def bench_prefill(args):
         del lins, xs
         torch.cuda.empty_cache()
     return res
+
+
+def bench_prefill_short(args, M=256):
+    """A short prompt through the whole config-3 layer (q, k, v, o, gate, up,
+    down; 4-bit NF4 + double quant, group 128): QuantLinear.forward, whose
+    fused kernel splits K across workgroups where its tiles would leave CUs
+    idle, against dequantize + hipBLASLt."""
+    import recipes
+    import tensorshrink_amd as ts
+    opts = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+    lins = []
+    for i, (name, n, k) in enumerate(recipes.LLAMA3_8B_LINEARS):
+        w = recipes.gaussian_weight(n, k, recipes.layer_seed(i))
+        lins.append((name, ts.QuantLinear(ts.quantize_tensor(w, **opts))))
+        del w
+    xs = {4096: recipes.activations(M, 4096).cuda(), 14336: recipes.activations(M, 14336).cuda()}
+    r = _timed_linears(lins, xs, M, lambda q, x: q(x), args.prefill_steps)
+    r["path"] = "QuantLinear.forward per linear (fused prefill kernel, K split where few tiles)"
+    lib_ref = _timed_linears(lins, xs, M, _forward_gemm, args.prefill_steps)
+    lib_ref["path"] = "library reference: dequantize into a workspace + one hipBLASLt GEMM"
+    r["library_reference"] = lib_ref
+    r["workload"] = (f"M={M} through the config-3 Llama-3-8B layer's 7 linears, 4-bit NF4 + double quant, "
+                     "group 128, outlier_frac 0.001")
+    _WS.clear()
+    del lins, xs
+    torch.cuda.empty_cache()
+    return r
 
 
 def bench_quantize(args):
@@ -567,7 +606,9 @@ def main():
         copy_calibration()
         return
     if args.prefill_only:
-        print(json.dumps({"prefill": bench_prefill(args)}), flush=True)
+        pre = bench_prefill(args)
+        pre["short_prompt"] = bench_prefill_short(args)
+        print(json.dumps({"prefill": pre}), flush=True)
         return
     import recipes
     opts = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
@@ -619,6 +660,9 @@ def main():
         log("prefill: M=2048")
         pre = bench_prefill(args)
         log(f"prefill: {pre}")
+        log("prefill: short prompt (M=256)")
+        pre["short_prompt"] = bench_prefill_short(args)
+        log(f"prefill short prompt: {pre['short_prompt']}")
     quant = None
     if not args.no_quantize:
         log("quantize: 28672x8192")
