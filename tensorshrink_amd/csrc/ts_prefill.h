@@ -87,6 +87,7 @@ struct PrefillArgs {
   // bias, into y.
   float* part;
   int32_t k_split;
+  int32_t bm, bn;  // the launch's tile (host side: the kernel has it as template arguments)
   // byte extents of the buffers read through buffer resources (all < 2^31)
   uint32_t x_bytes, p_bytes, meta_elems, dqm_bytes, s2_bytes, ocs_bytes;
 };
@@ -679,53 +680,67 @@ inline int launch_prefill(PrefillArgs a, hipStream_t st) {
 }
 
 // Launch shape of the prefill kernel for an M x N x K product of a layer
-// with `bits`-bit codes (cb: with a codebook). Tiles: 256 x 256 on 8 waves
-// when they fill the CUs, else 256 x 128 on 4 waves, or 128 x 128 when 256 x
-// 128 tiles would still leave CUs idle and 128 x 128 tiles fit one round.
-// K is split across k_split (1-8) workgroups per tile, at least 8 k-steps
-// each, where that is estimated faster: few tiles (narrow layers or few rows
-// at small M: 4096 x 14336 at M = 256 has 64 tiles for 256 CUs) or a partial
-// last round of deep tiles. Estimate, from MI355X measurements: workgroups
-// per CU (rounded up) x k-steps per split x the tile's k-step time (1.25 us
-// for 128 x 128, 1.75 for 256 x 128, 2.9 for 256 x 256), where two 128 x 128
-// workgroups whose LDS fits one CU together share it at 1.5x the time of
-// one; plus, with splits, the fp32 partial sums' HBM traffic (k_split * M *
-// N * 4 bytes written and read, at 4 TB/s) and 2 us for the reduction
-// launch. A split must win by 3 %. The partials stay below the GEMM library
-// path's workspace (rows x cols x 2 + 32 MB).
+// with `bits`-bit codes (cb: with a codebook): the tile (256 x 256 on 8
+// waves, 256 x 128 on 4, 128 x 128 on 4) and the number of workgroups K is
+// split across per tile (1-8, at least 8 k-steps each). The choice comes from
+// an estimate calibrated on MI355X by forced sweeps (4 layer shapes x NF4 /
+// NF8 / RVQ x M = 129-4096):
+//   workgroups per CU (rounded up)
+//     x (k-steps per split x the tile's k-step time + 6 us of prologue and
+//        epilogue), k-step times 2.6 / 1.75 / 1.2 us;
+//     two 128 x 128 workgroups whose LDS fits one CU together share it at
+//     1.5x the time of one;
+//   + with splits: the fp32 partial sums' HBM traffic (k_split * M * N * 4
+//     bytes written and read, at 4 TB/s) and 2 us for the reduction launch.
+// The incumbent is the tile that fills the CUs unsplit (256 x 256 when those
+// tiles do, else 256 x 128, or 128 x 128 when 256 x 128 tiles would leave
+// CUs idle and 128 x 128 tiles fit one round); another choice must be
+// estimated 3 % faster. Splits pay where tiles are few (narrow layers or
+// small M: 4096 x 14336 at M = 256 has 32 tiles of 256 x 128 for 256 CUs)
+// and where they let the 256 x 256 tile fill the CUs (the same layer at M =
+// 2048: 128 such tiles, two splits). The partials stay below the GEMM
+// library path's workspace (rows x cols x 2 + 32 MB). split_ok = false (no
+// workspace for the partials): the best unsplit tile.
 struct PrefillPlan {
   int bm, bn;
   int64_t tiles;
   int splits;
 };
-inline PrefillPlan prefill_plan(int64_t M, int64_t N, int64_t K, int bits, bool cb) {
-  PrefillPlan p{};
-  if (ts_cdiv(M, PF_BM) * ts_cdiv(N, 256) >= PF_CUS) {
-    p.bm = 256; p.bn = 256;
-  } else if (ts_cdiv(M, PF_BM) * ts_cdiv(N, 128) < PF_CUS && ts_cdiv(M, 128) * ts_cdiv(N, 128) <= PF_CUS) {
-    p.bm = 128; p.bn = 128;
-  } else {
-    p.bm = 256; p.bn = 128;
-  }
-  p.tiles = ts_cdiv(M, p.bm) * ts_cdiv(N, p.bn);
-  p.splits = 1;
+inline PrefillPlan prefill_plan(int64_t M, int64_t N, int64_t K, int bits, bool cb, bool split_ok = true) {
+  struct Shape {
+    int bm, bn;
+    double tk;  // us per k-step of one workgroup
+  };
+  constexpr Shape shapes[3] = {{256, 256, 2.6}, {256, 128, 1.75}, {128, 128, 1.2}};
+  int inc;  // the incumbent shape
+  if (ts_cdiv(M, 256) * ts_cdiv(N, 256) >= PF_CUS) inc = 0;
+  else if (ts_cdiv(M, 256) * ts_cdiv(N, 128) < PF_CUS && ts_cdiv(M, 128) * ts_cdiv(N, 128) <= PF_CUS) inc = 2;
+  else inc = 1;
   // (the LDS size of prefill_smem<bits, cb, 128, 128>; registers allow two
   // such workgroups per CU, but not two of the larger tiles)
   const size_t lds128 = (size_t)2 * 256 * PF_BK * 2 + (cb ? ((size_t)1 << bits) * 32 * 4 : 0);
-  const bool pair = p.bm == 128 && 2 * lds128 <= 160 * 1024;
-  const double tk = p.bn == 256 ? 2.9 : (p.bm == 256 ? 1.75 : 1.25);
   const int64_t KT = K / PF_BK;
   const double cap = (double)N * (double)K * 2 + (double)(32 << 20);
-  double best = 0;
-  for (int s = 1; s <= PF_SPLIT_MAX; ++s) {
-    if (s > 1 && (KT / s < PF_SPLIT_MIN_KT || (double)s * M * N * 4 >= cap)) break;
-    const int64_t wpc = ts_cdiv(p.tiles * s, PF_CUS);
+  auto estimate = [&](const Shape& sh, int s) {
+    const int64_t tiles = ts_cdiv(M, sh.bm) * ts_cdiv(N, sh.bn);
+    const bool pair = sh.bm == 128 && 2 * lds128 <= 160 * 1024;
+    const int64_t wpc = ts_cdiv(tiles * s, PF_CUS);
     const double rounds = pair ? (double)(wpc / 2) * 1.5 + (double)(wpc % 2) : (double)wpc;
-    double t = rounds * (double)ts_cdiv(KT, s) * tk;
+    double t = rounds * ((double)ts_cdiv(KT, s) * sh.tk + 6.0);
     if (s > 1) t += ((double)s * M * N * 8 + (double)M * N * 2) * 1e6 / 4e12 + 2.0;
-    if (s == 1 || t < 0.97 * best) {
-      best = t;
-      p.splits = s;
+    return t;
+  };
+  PrefillPlan p{shapes[inc].bm, shapes[inc].bn, ts_cdiv(M, shapes[inc].bm) * ts_cdiv(N, shapes[inc].bn), 1};
+  double best = estimate(shapes[inc], 1);
+  for (int i = 0; i < 3; ++i) {
+    for (int s = 1; s <= (split_ok ? PF_SPLIT_MAX : 1); ++s) {
+      if (s > 1 && (KT / s < PF_SPLIT_MIN_KT || (double)s * M * N * 4 >= cap)) break;
+      if (i == inc && s == 1) continue;
+      const double t = estimate(shapes[i], s);
+      if (t < 0.97 * best) {
+        best = t;
+        p = PrefillPlan{shapes[i].bm, shapes[i].bn, ts_cdiv(M, shapes[i].bm) * ts_cdiv(N, shapes[i].bn), s};
+      }
     }
   }
   return p;
@@ -737,16 +752,16 @@ inline size_t prefill_part_bytes(const PrefillPlan& p, int64_t M, int64_t N) {
 // y = sum of the K splits' fp32 sums (+ bias), cast to y's dtype.
 int launch_splitk_reduce(const PrefillArgs& a, bool bf16, hipStream_t st);
 
-// a.part / a.k_split: set by the caller (k_split = 1 without workspace)
+// a.bm / a.bn / a.part / a.k_split: the caller's plan (k_split = 1 without
+// workspace)
 template <int BITS, int GS, bool BF16, bool CB, bool RVQ>
 inline int launch_prefill_tiles(PrefillArgs& a, hipStream_t st) {
   const bool dq = a.dqsc != nullptr;
-  const PrefillPlan p = prefill_plan(a.M, a.N, a.K, BITS, CB);
   int rc;
-  if (p.bn == 256) {
+  if (a.bn == 256) {
     rc = dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 256, PF_NW_WIDE>(a, st)
             : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 256, PF_NW_WIDE>(a, st);
-  } else if (p.bm == 128) {
+  } else if (a.bm == 128) {
     rc = dq ? launch_prefill<BITS, GS, BF16, CB, RVQ, true, 128, 4, 128>(a, st)
             : launch_prefill<BITS, GS, BF16, CB, RVQ, false, 128, 4, 128>(a, st);
   } else {

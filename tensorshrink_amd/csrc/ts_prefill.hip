@@ -122,15 +122,20 @@ int prefill_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ld
   a.meta_elems = (uint32_t)meta;
   a.dqm_bytes = (uint32_t)dqm;
   a.s2_bytes = (uint32_t)s2;
-  // K split when the plan asks for one and the workspace holds the partials
-  const PrefillPlan plan = prefill_plan(M, L->rows, L->padded_cols, prefill_bits(L), prefill_codebook(L));
+  // K split when the plan asks for one and the workspace holds the partials;
+  // else the best unsplit tile
+  PrefillPlan plan = prefill_plan(M, L->rows, L->padded_cols, prefill_bits(L), prefill_codebook(L));
   const size_t pb = prefill_part_bytes(plan, M, L->rows);
   a.k_split = 1;
   a.part = nullptr;
   if (pb > 0 && ws && ws_bytes >= pb && (reinterpret_cast<uintptr_t>(ws) & 15) == 0) {
     a.k_split = plan.splits;
     a.part = static_cast<float*>(ws);
+  } else if (plan.splits > 1) {
+    plan = prefill_plan(M, L->rows, L->padded_cols, prefill_bits(L), prefill_codebook(L), false);
   }
+  a.bm = plan.bm;
+  a.bn = plan.bn;
   const bool bf16 = x_dtype == TS_BF16;
   switch (L->bits * 1000 + L->group_size) {
     case 2064: return prefill_b2_g64(L, a, bf16, st);

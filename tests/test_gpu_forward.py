@@ -420,12 +420,15 @@ def _dense_row_weight(rows, cols, seed):
     (dict(bits=6, group_size=128, double_quant=True), 512, 8192, 160, torch.bfloat16, True),
     (dict(bits=2, group_size=64, double_quant=True), 1002, 2048, 140, torch.float16, True),
     (dict(bits=4, group_size=64), 1024, 4096, 2048, torch.float16, False),
+    (dict(bits=8, group_size=128, double_quant=True, nf_quant=True), 3072, 4096, 1024, torch.bfloat16, True),
+    (dict(bits=6, group_size=128, double_quant=True), 3072, 4096, 1024, torch.float16, False),
 ])
 def test_forward_split_k(fmt, rows, cols, M, xdt, bias):
-    """Layers whose prefill tiles fill at most half of the CUs: QuantLinear
-    hands the fused kernel a workspace for K-split partial sums; the split
-    result (with dense outlier rows, bias, fp16 / bf16) meets the float64
-    product and agrees with the unsplit kernel."""
+    """Shapes whose launch plan splits K (128 x 128, 256 x 128 and, at
+    3072 x 4096 with M = 1024, 256 x 256 tiles on 8 waves): QuantLinear
+    hands the fused kernel a workspace for the partial sums; the split result
+    (with dense outlier rows, bias, fp16 / bf16) meets the float64 product
+    and agrees with the unsplit kernel."""
     ts = _ts()
     from tensorshrink_amd import _lib as L
     w = _dense_row_weight(rows, cols, 900 + rows)

@@ -189,11 +189,10 @@ def test_forward_workspace_bytes():
 
 def test_forward_partials_bytes():
     """Host-only sizing of the fused prefill kernel's K-split workspace,
-    k_split x M x rows x 4 bytes: 0 at decode sizes, where the tiles fill the
-    CUs and where K is too short to split; the split counts the launch plan
-    picks for few tiles (two 4-wave 128 x 128 workgroups share a CU when their
-    LDS fits, which NF8's 256-entry codebook copies prevent); always below
-    the GEMM path's workspace. No GPU call."""
+    k_split x M x rows x 4 bytes: 0 at decode sizes, where unsplit tiles fill
+    the CUs and where K is too short to split; the split counts the launch
+    plan picks for few tiles and for 256 x 256 tiles that two splits let fill
+    the CUs; always below the GEMM path's workspace. No GPU call."""
     import ctypes
     L, lib = _lib()
     fake = ctypes.c_void_p(0x1000)  # never dereferenced by the sizing call
@@ -217,10 +216,12 @@ def test_forward_partials_bytes():
             assert n < lib.ts_forward_workspace_bytes(ctypes.byref(layer(rows, cols, **kw)), M)
         return k
 
-    # down projection at M = 256: 64 tiles of 128 x 128
+    # down projection at M = 256: 32 tiles of 256 x 128
     assert splits(4096, 14336, 256) == 8
-    assert splits(4096, 14336, 256, bits=8, codebook=True) == 4
-    # k / v at M = 2048: 128 tiles
+    assert splits(4096, 14336, 256, bits=8, codebook=True) == 8
+    # ... and at M = 2048 (config 4): 128 tiles of 256 x 256, two splits
+    assert splits(4096, 14336, 2048, bits=8, codebook=True) == 2
+    # k / v at M = 2048: 64 tiles of 256 x 128
     assert splits(1024, 4096, 2048) == 4
     # 512 x 8192 at M = 160: 8 tiles, 128 k-steps
     assert splits(512, 8192, 160) == 8
