@@ -412,7 +412,8 @@ def bench_prefill(args):
 
         r = timed(lambda q, x: q(x))
         r["path"] = ("QuantLinear.forward: the fused dequant-into-LDS MFMA kernel (ts::prefill_kernel, "
-                     "256x256 tiles, 8 waves)")
+                     "256x256 tiles, 8 waves; the down projection's K split in two, fp32 partials + one "
+                     "reduction pass)")
         lib_ref = timed(_forward_gemm)
         lib_ref["path"] = "library reference: dequantize into a workspace + one hipBLASLt GEMM"
         r["library_reference"] = lib_ref

@@ -106,8 +106,9 @@ size_t ts_forward_workspace_bytes(const ts_qlayer* layer, int64_t M);
  * fused prefill kernel splits K across workgroups for M activation rows: the
  * splits' fp32 partial sums, k_split x M x rows x 4 bytes, k_split <= 8. Not 0
  * only where the launch plan estimates a split faster: tiles that would leave
- * compute units idle (few rows or small M, e.g. 4096 x 14336 at M = 256) or a
- * partial last round of deep tiles. 0 where the decode kernel runs. Always below
+ * compute units idle (few rows or small M, e.g. 4096 x 14336 at M = 256), or
+ * 256 x 256 tiles that fill them only when split (the same layer at M =
+ * 2048). 0 where the decode kernel runs. Always below
  * ts_forward_workspace_bytes(layer, M), so a workspace of this size never
  * selects the GEMM library path. No counterpart in the reference (its Triton
  * kernels do not split K). */
