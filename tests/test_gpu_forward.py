@@ -454,7 +454,8 @@ def test_forward_split_k(fmt, rows, cols, M, xdt, bias):
 def test_forward_split_k_f32_strided():
     """The K-split path through the C-ABI: fp32 output with a row stride past
     the layer's rows (the stride tail stays untouched), two calls in a row
-    sharing one workspace, the second with fewer rows."""
+    sharing one workspace, the second with fewer rows and a bias (added in the
+    reduction pass)."""
     ts = _ts()
     from tensorshrink_amd import _lib as L
     rows, cols, ldy = 1024, 4096, 1100
@@ -462,15 +463,16 @@ def test_forward_split_k_f32_strided():
     W = ql.dequantize_weight(torch.float32).double()
     lib, lay = L.load(), ctypes.byref(ql._layer)
     ws = torch.empty(lib.ts_forward_partials_bytes(lay, 300), dtype=torch.uint8, device="cuda")
-    for M in (300, 150):
+    bias = (torch.randn(rows, generator=torch.Generator().manual_seed(9)) * 0.5).to(torch.bfloat16).cuda()
+    for M, b in ((300, None), (150, bias)):
         need = lib.ts_forward_partials_bytes(lay, M)
         assert 0 < need <= ws.numel()
         x = recipes.activations(M, cols, seed=M).cuda()
         y = torch.full((M, ldy), 7.0, dtype=torch.float32, device="cuda")
         L.check(lib.ts_qlinear_forward(lay, x.data_ptr(), M, cols, L.dtype_code(x.dtype), y.data_ptr(), ldy,
-                                       L.dtype_code(torch.float32), None, ws.data_ptr(), ws.numel(),
+                                       L.dtype_code(torch.float32), L.ptr(b), ws.data_ptr(), ws.numel(),
                                        L.stream_ptr()), "split fwd")
-        y_ref = x.double() @ W.T
+        y_ref = x.double() @ W.T + (b.double() if b is not None else 0)
         assert max_rel_err(y[:, :rows], y_ref) <= TOL
         assert bool((y[:, rows:] == 7.0).all())
 
