@@ -28,6 +28,9 @@ Alongside it (extra keys of the same JSON line):
   * "cfg1"           - BASELINE config 1: the 4096x4096 linear by itself at
                        M = 1 and 16, each line with the reference CPU fallback
                        forward of the same layer timed beside it;
+  * "cfg2"           - BASELINE config 2: the 11008x4096 2-bit companded
+                       (Lloyd-Max) linear by itself at M = 1, 4 and 8, with the
+                       reference CPU fallback forward beside each line;
   * "decode_cfg5"    - the same decode step on BASELINE config 5's 70B layer
                        (its 8/4/2-bit mix), 3 rotating copies (1.4 GB);
   * "prefill"        - BASELINE config 4: gate/up/down at M=2048, 8-bit NF8 + DQ
@@ -246,6 +249,30 @@ def bench_single(copies, idx: int, M: int, reps: int):
     nb = layer_bytes(q0, M)
     return {"M": M, "bytes": nb, "us": round(us, 2), "GBps": round(nb / (us * 1e-6) / 1e9, 1),
             "frac_of_hbm_peak": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_cfg2(args, n_copies=24):
+    """one 11008x4096 QuantLinear, 2-bit companded
+    (Lloyd-Max codebook fitted per tensor), group 64, outlier_frac 0.001,
+    Student-t(5) x 0.02 weights (the test suite's seeds), at M = 1, 4 and 8.
+    24 rotating copies (about 310 MB) so that a replay does not find its
+    weights in the 256 MB MALL."""
+    import recipes
+    import tensorshrink_amd as ts
+    torch.manual_seed(2024)  # the Lloyd-Max fit samples from the global RNG
+    w = recipes.student_t_weight(11008, 4096, 2000)
+    base = ts.QuantLinear(ts.quantize_tensor(w, bits=2, group_size=64, outlier_frac=0.001, companded=True))
+    del w
+    copies = [[("cfg2", base)]] + [[("cfg2", clone_layer(base))] for _ in range(n_copies - 1)]
+    lines = [bench_single(copies, 0, M, args.kernel_reps * 3) for M in (1, 4, 8)]
+    if not args.no_cpu:
+        for line in lines:
+            line["cpu_baseline"] = cpu_forward_baseline(base, line["M"], min(args.cpu_budget, 8.0))
+    del copies
+    torch.cuda.empty_cache()
+    return {"workload": "BASELINE config 2: single QuantLinear 11008x4096, 2-bit companded (Lloyd-Max), group 64, "
+                        "outlier_frac 0.001, Student-t(5) weights; one launch per forward, 24 rotating copies",
+            "lines": lines}
 
 
 def cpu_forward_baseline(ql, M: int, budget_s: float):
@@ -636,6 +663,8 @@ def main():
         for line in cfg1["lines"]:
             line["cpu_baseline"] = cpu_forward_baseline(copies[0][0][1], line["M"], min(args.cpu_budget, 8.0))
     log(f"cfg1: {cfg1['lines']}")
+    cfg2 = bench_cfg2(args)
+    log(f"cfg2: {cfg2['lines']}")
     k_us = sum(v["us"] for v in kern.values())
     achieved = dec["step_bytes"] / (dec["step_gpu_us"] * 1e-6) / 1e9
     log(f"decode: {dec['ms_per_step'] * 1e3:.1f} us/step, {dec['value']:.0f} GB/s; GPU {dec['step_gpu_us']:.1f} "
@@ -707,6 +736,7 @@ def main():
                      "traffic_per_launch": traffic["per_launch_bytes"] if traffic else None},
         "decode_drop_in" if not args.ungrouped else "decode_grouped": alt_line,
         "cfg1": cfg1,
+        "cfg2": cfg2,
         "decode_cfg5": d70,
         "prefill": pre,
         "quantize": quant,
