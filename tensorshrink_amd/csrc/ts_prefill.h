@@ -48,6 +48,7 @@
 #pragma once
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "ts_common.h"
 
@@ -619,39 +620,90 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   if (kt < KT) kstep(kt, S1, S0);
   }
 
-  // epilogue: bias, cast, store (a K split: its fp32 sums)
-  if (P > 1) {
-    float* pp = a.part + (int64_t)split * a.M * a.N;
+  // ---- epilogue: bias, cast, store (a K split: its fp32 sums) ---------------
+  // A lane's accumulators are 16 values of one output column (rows
+  // 8 (r >> 2) + 4 (lane >> 5) + (r & 3) of a 32-row block): stored as they
+  // are, every store instruction writes one 2- or 4-byte element per lane.
+  // Each wave instead stages one 32 x 32 TN block at a time in a private LDS
+  // region (the operand buffers are free once every wave is past the
+  // barrier) and stores whole 16-byte row chunks. Outputs whose rows are not
+  // 16-byte aligned take the element-wise path.
+  const bool f32out = P > 1 || a.y_dtype == TS_F32;
+  const int esz = f32out ? 4 : 2;
+  char* const dst_base =
+      P > 1 ? reinterpret_cast<char*>(a.part + (int64_t)split * a.M * a.N) : static_cast<char*>(a.y);
+  const int64_t ld = P > 1 ? a.N : a.ldy;
+  const int64_t mw = m0 + wm * (BM / 2), nw = n0 + wn * (BN / WN);  // the wave's first row and column
+  if ((reinterpret_cast<uintptr_t>(dst_base) & 15) == 0 && (ld * esz) % 16 == 0) {
+    constexpr int SC = 32 * TN;  // columns of a wave block
+    constexpr int SS = SC + 8;   // staged row stride in elements: rows r and r + 4 sit 32 banks apart
+    static_assert(NW * 32 * SS * 4 <= 2 * (BM + BN) * PF_BK * 2, "staging fits the operand buffers");
+    ts_lds_barrier();  // every wave is past its last operand read
+    char* const stage = reinterpret_cast<char*>(smem) + wave * (32 * SS * 4);
+    float bv[TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int64_t n = n0 + wn * (BN / WN) + 32 * j + (lane & 31);
-      if (n >= a.N) continue;
+      const int64_t n = nw + 32 * j + (lane & 31);
+      bv[j] = (P == 1 && a.bias && n < a.N) ? XT<BF16>::to_f(a.bias[n]) : 0.f;
+    }
+    // ESZ: bytes per staged element (4: fp32 partials or output, 2: bf16/f16)
+    auto blocks = [&](auto esz_c) {
+      constexpr int ESZ = decltype(esz_c)::value;
+      constexpr int CPR = SC * ESZ / 16;  // 16-byte chunks per row
+      constexpr int EPC = 16 / ESZ;       // elements per chunk
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (m < a.M) pp[m * a.N + n] = acc[i][j][r];
+        for (int j = 0; j < TN; ++j) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), col = 32 * j + (lane & 31);
+            const float v = acc[i][j][r] + bv[j];
+            if constexpr (ESZ == 4) reinterpret_cast<float*>(stage)[row * SS + col] = v;
+            else reinterpret_cast<uint16_t*>(stage)[row * SS + col] = XT<BF16>::from_f(v);
+          }
+        }
+        // (one wave's LDS accesses complete in order: the reads see the
+        // writes above, and the next block's writes come after these reads)
+#pragma unroll
+        for (int k = 0; k < 32 * CPR / 64; ++k) {
+          const int c = lane + 64 * k;
+          const int row = c / CPR, ch = c % CPR;
+          const int64_t m = mw + 32 * i + row, n = nw + ch * EPC;
+          if (m >= a.M) continue;
+          const ts_u32x4 v = *reinterpret_cast<const ts_u32x4*>(stage + row * SS * ESZ + ch * 16);
+          char* const dst = dst_base + (m * ld + n) * ESZ;
+          if (n + EPC <= a.N) {
+            *reinterpret_cast<ts_u32x4*>(dst) = v;
+          } else {  // the last chunk of a ragged row
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            for (int e = 0; e < EPC && n + e < a.N; ++e) {
+              if constexpr (ESZ == 4) reinterpret_cast<uint32_t*>(dst)[e] = w[e];
+              else reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            }
+          }
         }
       }
-    }
+    };
+    if (f32out) blocks(std::integral_constant<int, 4>{});
+    else blocks(std::integral_constant<int, 2>{});
     return;
   }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int64_t n = n0 + wn * (BN / WN) + 32 * j + (lane & 31);
+    const int64_t n = nw + 32 * j + (lane & 31);
     if (n >= a.N) continue;
-    const float b = a.bias ? XT<BF16>::to_f(a.bias[n]) : 0.f;
+    const float b = (P == 1 && a.bias) ? XT<BF16>::to_f(a.bias[n]) : 0.f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int64_t m = mw + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m >= a.M) continue;
         const float v = acc[i][j][r] + b;
-        const int64_t off = m * a.ldy + n;
-        if (a.y_dtype == TS_F32) reinterpret_cast<float*>(a.y)[off] = v;
-        else reinterpret_cast<uint16_t*>(a.y)[off] = XT<BF16>::from_f(v);
+        char* const dst = dst_base + (m * ld + n) * esz;
+        if (f32out) *reinterpret_cast<float*>(dst) = v;
+        else *reinterpret_cast<uint16_t*>(dst) = XT<BF16>::from_f(v);
       }
     }
   }
