@@ -438,17 +438,33 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   auto fetch_outlier = [&]() { tld = oload(min(ptr, oend > 0 ? oend - 1 : 0u)); };
 
   // ---- prologue --------------------------------------------------------------
+  // The row's outlier range is loaded first (unconditionally, through a
+  // buffer resource that reads zeros without outliers): its dependent chain
+  // (range -> first entry -> next entry) then overlaps the stage loads
+  // instead of starting after they land.
+  const __amdgpu_buffer_rsrc_t rop = ts_rsrc(a.orow_ptr, a.has_out ? (uint32_t)(4 * (a.N + 1)) : 4u);
+  const int64_t orow = min(n0 + wr, a.N);  // a row past N has an empty range
+  const uint32_t rb0 = ts_bld4(rop, (uint32_t)(4 * orow));
+  const uint32_t re0 = ts_bld4(rop, (uint32_t)(4 * min(orow + 1, a.N)));
   Stage S0, S1;
   load_x(0, X);
   load_stage(0, S0);
   load_stage(1, S1);
   if constexpr (CB) {
-    for (int i = tid; i < CBN * CBC; i += NT) cbs[i] = ts_f2h(a.codebook[i / CBC]);
+    // 16-byte chunks of 4 copies: chunk i holds copies of entry i / (CBC / 4);
+    // every thread runs the same trip count (a trailing thread rewrites the
+    // last chunk with the same value), so no load sits behind a branch
+    constexpr int CH = CBN * CBC / 4;
+#pragma unroll
+    for (int k = 0; k < (CH + NT - 1) / NT; ++k) {
+      const int i = min(tid + k * NT, CH - 1);
+      const uint32_t h = ts_f2h(a.codebook[i / (CBC / 4)]);
+      *reinterpret_cast<ts_u32x4*>(cbs + 4 * i) = ts_u32x4{h, h, h, h};
+    }
   }
   if (a.has_out) {
-    const int64_t r = min(n0 + wr, a.N);  // a row past N has an empty range
-    uint32_t rb = (uint32_t)a.orow_ptr[r];
-    oend = (uint32_t)a.orow_ptr[min(r + 1, a.N)];
+    uint32_t rb = rb0;
+    oend = re0;
     if (kt0 > 0) {
       // a later K split starts at the row's first entry with column >=
       // kt0 * BK: count the entries before it among the next 16 (one round
