@@ -751,15 +751,16 @@ inline int launch_prefill(PrefillArgs a, hipStream_t st) {
 // with `bits`-bit codes (cb: with a codebook): the tile (256 x 256 on 8
 // waves, 256 x 128 on 4, 128 x 128 on 4) and the number of workgroups K is
 // split across per tile (1-8, at least 8 k-steps each). The choice comes from
-// an estimate calibrated on MI355X by forced sweeps (4 layer shapes x NF4 /
-// NF8 / RVQ x M = 129-4096):
+// an estimate fitted on MI355X to forced sweeps (618 launches: 4 layer shapes
+// x NF4 / NF8 x M = 256-2048 x every tile x 1-8 splits; 5 % rms error):
 //   workgroups per CU (rounded up)
-//     x (k-steps per split x the tile's k-step time + 6 us of prologue and
-//        epilogue), k-step times 2.6 / 1.75 / 1.2 us;
+//     x (k-steps per split x the tile's k-step time + 2.3 us of prologue and
+//        epilogue), k-step times 2.05 / 1.4 / 1.12 us;
 //     two 128 x 128 workgroups whose LDS fits one CU together share it at
-//     1.5x the time of one;
+//     1.4x the time of one;
 //   + with splits: the fp32 partial sums' HBM traffic (k_split * M * N * 4
-//     bytes written and read, at 4 TB/s) and 2 us for the reduction launch.
+//     bytes written and read, at 5.7 TB/s) and 7.5 us for the reduction
+//     pass.
 // The incumbent is the tile that fills the CUs unsplit (256 x 256 when those
 // tiles do, else 256 x 128, or 128 x 128 when 256 x 128 tiles would leave
 // CUs idle and 128 x 128 tiles fit one round); another choice must be
@@ -779,7 +780,7 @@ inline PrefillPlan prefill_plan(int64_t M, int64_t N, int64_t K, int bits, bool 
     int bm, bn;
     double tk;  // us per k-step of one workgroup
   };
-  constexpr Shape shapes[3] = {{256, 256, 2.6}, {256, 128, 1.75}, {128, 128, 1.2}};
+  constexpr Shape shapes[3] = {{256, 256, 2.05}, {256, 128, 1.4}, {128, 128, 1.12}};
   int inc;  // the incumbent shape
   if (ts_cdiv(M, 256) * ts_cdiv(N, 256) >= PF_CUS) inc = 0;
   else if (ts_cdiv(M, 256) * ts_cdiv(N, 128) < PF_CUS && ts_cdiv(M, 128) * ts_cdiv(N, 128) <= PF_CUS) inc = 2;
@@ -793,9 +794,9 @@ inline PrefillPlan prefill_plan(int64_t M, int64_t N, int64_t K, int bits, bool 
     const int64_t tiles = ts_cdiv(M, sh.bm) * ts_cdiv(N, sh.bn);
     const bool pair = sh.bm == 128 && 2 * lds128 <= 160 * 1024;
     const int64_t wpc = ts_cdiv(tiles * s, PF_CUS);
-    const double rounds = pair ? (double)(wpc / 2) * 1.5 + (double)(wpc % 2) : (double)wpc;
-    double t = rounds * ((double)ts_cdiv(KT, s) * sh.tk + 6.0);
-    if (s > 1) t += ((double)s * M * N * 8 + (double)M * N * 2) * 1e6 / 4e12 + 2.0;
+    const double rounds = pair ? (double)(wpc / 2) * 1.4 + (double)(wpc % 2) : (double)wpc;
+    double t = rounds * ((double)ts_cdiv(KT, s) * sh.tk + 2.3);
+    if (s > 1) t += ((double)s * M * N * 8 + (double)M * N * 2) * 1e6 / 5.7e12 + 7.5;
     return t;
   };
   PrefillPlan p{shapes[inc].bm, shapes[inc].bn, ts_cdiv(M, shapes[inc].bm) * ts_cdiv(N, shapes[inc].bn), 1};

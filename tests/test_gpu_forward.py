@@ -485,17 +485,17 @@ def test_forward_prefill_ragged_rows_strided(split):
     stored element by element and the stride tail stays untouched; bf16 and
     fp32 outputs, with and without the K-split workspace."""
     from tensorshrink_amd import _lib as L
-    ql, W = _layer(1018, 1024, 95, NF4)
+    ql, W = _layer(1018, 2048, 95, NF4)
     lib, lay = L.load(), ctypes.byref(ql._layer)
     M = 300
-    x = recipes.activations(M, 1024, seed=5).cuda()
+    x = recipes.activations(M, 2048, seed=5).cuda()
     ref = x.float() @ W.T
     nws = lib.ts_forward_partials_bytes(lay, M) if split else 0
     assert (nws > 0) == split
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device="cuda")
     for ydt, ldy in ((torch.bfloat16, 1024), (torch.float32, 1020)):
         y = torch.full((M, ldy), 7.0, dtype=ydt, device="cuda")
-        L.check(lib.ts_qlinear_forward(lay, x.data_ptr(), M, 1024, L.TS_BF16, y.data_ptr(), ldy, L.dtype_code(ydt),
+        L.check(lib.ts_qlinear_forward(lay, x.data_ptr(), M, 2048, L.TS_BF16, y.data_ptr(), ldy, L.dtype_code(ydt),
                                        None, ws.data_ptr() if split else None, nws, L.stream_ptr()), "fwd")
         assert max_rel_err(y[:, :1018].float(), ref) <= TOL, ydt
         assert bool((y[:, 1018:] == 7.0).all()), ydt
