@@ -8,15 +8,18 @@
 // the tile's outliers into it and feeds MFMA f32_32x32x16 with fp32
 // accumulation.
 //
-// Tiles of 256 x BN x 64. BN = 256 (when the tiles fill the CUs): 8 waves,
-// two per SIMD, as a 2 x 4 grid of 128 x 64 wave tiles (4 x 2 MFMA blocks of
-// 32 x 32); BN = 128: 4 waves, one per SIMD, 2 x 2 grid of 128 x 64 (or of
-// 64 x 64 with 128-row tiles, when 256-row tiles would leave CUs idle). Each
-// weight element is dequantized once per workgroup. Sized from gfx950
-// measurements: a 32x32x16 MFMA occupies a SIMD for 32 cycles; the LDS serves
-// ds_read_b128 at about 190 B per cycle, ds_write_b128 at half that, and a
-// 64-lane codebook lookup (ds_read_u16) costs about as much as a b128 read,
-// so NF8's 256 lookups per k-step are the largest single LDS cost.
+// Tiles of BM x BN x 64: 256 x 256 on 8 waves, two per SIMD, as a 2 x 4
+// grid of 128 x 64 wave tiles (4 x 2 MFMA blocks of 32 x 32); 256 x 128 on 4
+// waves, one per SIMD, 2 x 2 grid of 128 x 64; 128 x 128 on 4 waves (64 x 64
+// wave tiles). A launch plan (prefill_plan) picks the tile and a split of K
+// across up to 8 workgroups per tile, whose fp32 partial sums one reduction
+// pass adds up. Each weight element is dequantized once per workgroup; each
+// wave stores its outputs as 16-byte row chunks staged through LDS. Sized
+// from gfx950 measurements: a 32x32x16 MFMA occupies a SIMD for 32 cycles;
+// the LDS serves ds_read_b128 at about 190 B per cycle, ds_write_b128 at
+// half that, and a 64-lane codebook lookup (ds_read_u16) costs about as much
+// as a b128 read, so NF8's 256 lookups per k-step are the largest single LDS
+// cost.
 //   * All global reads are raw buffer loads (64-bit bases in SGPRs, 32-bit
 //     offsets) into register stages: weights two k-steps ahead, x one.
 //     No load the compiler tracks is conditional, so its wait counts stay
