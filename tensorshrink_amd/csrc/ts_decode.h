@@ -1163,6 +1163,12 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
       if (xreg(16)) TS_DEC(XM_REG, DQV, true, 16, UMAX, false);                  \
       TS_DEC(XM_DMA, DQV, true, 16, UMAX, false);                                \
     }                                                                            \
+    /* x from L2 on launches whose rows fit two batches per wave of 8: the */   \
+    /* straight-line kernel (config 1 at M = 16: 12.4 -> 11.7 us) */           \
+    if (!xlds && sh.ok && alm && sh.W == 8) {                                    \
+      if (one) TS_DEC1(XM_GLOBAL, DQV, true, 8, UMAX);                           \
+      TS_DEC(XM_GLOBAL, DQV, true, 8, UMAX, false);                              \
+    }                                                                            \
     if (xlds && alm) TS_DEC(XM_DMA, DQV, true, 16, UMAX, true);                  \
     if (xlds) TS_DEC(XM_DMA, DQV, false, 16, UMAX, true);                        \
     if (alm) TS_DEC(XM_GLOBAL, DQV, true, 16, UMAX, true);                       \

@@ -501,6 +501,22 @@ def test_forward_prefill_ragged_rows_strided(split):
         assert bool((y[:, 1018:] == 7.0).all()), ydt
 
 
+@pytest.mark.parametrize("opts", [NF4, dict(bits=2, group_size=64, outlier_frac=0.002, double_quant=True)])
+def test_forward_decode_x_from_l2(opts):
+    """Decode at 9-16 rows with x too large for LDS on layers whose rows fit
+    two batches per wave of 8: the 8-wave straight-line launches that read x
+    from L2, with one batch per wave (2048 x 4096) and two (4112 x 8192, 257
+    row tiles), against the dequantized weight's float32 product."""
+    ts = _ts()
+    for rows, cols in ((2048, 4096), (4112, 8192)):
+        ql = ts.QuantLinear(ts.quantize_tensor(recipes.gaussian_weight(rows, cols, 94), **opts))
+        W = ql.dequantize_weight(torch.float32)
+        for M in (9, 12, 16):
+            x = recipes.activations(M, cols, seed=M).cuda()
+            assert max_rel_err(ql(x).float(), x.float() @ W.T) <= TOL, (rows, M)
+        del ql, W
+
+
 def test_forward_group_fallbacks():
     """Mixed formats, M > 32, and 17-32 rows on layers of more than 12288
     rows in all run one forward per layer."""
