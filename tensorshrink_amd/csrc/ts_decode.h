@@ -1071,7 +1071,7 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   constexpr int UMAX = DecGeom<BITS, GS, RVQ>::UMAX;
   constexpr int UMB = UMAX >= 2 ? UMAX / 2 : 1;  // batches of the multi-block (M > 16) launches: registers
   const DecodeArgs& a = g.a[0];
-  const bool xlds = (size_t)a.M * a.K * 2 <= DEC_XLDS_MAX;
+  const bool xfit = (size_t)a.M * a.K * 2 <= DEC_XLDS_MAX;
   const bool dq = a.dqsc != nullptr;
   for (int l = 0; l < g.n; ++l)
     if (dq && g.a[l].dq_gs < (uint32_t)UMAX) return TS_NOT_COVERED;  // a batch would span > 2 super-groups
@@ -1090,6 +1090,21 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
     return al;
   };
   const DecShape sh = decode_shape(g.tile_end[g.n - 1], a.n_groups, UMAX);
+  // x from global memory at M > 1 with at least half a resident round of
+  // waves: two row tiles per workgroup share each x fragment (4-bit codes),
+  // W the smallest of {4, 8, 16} that gives one batch per wave
+  constexpr bool RT2_OK = BITS == 4 && !RVQ && !CB8 && DecGeom<BITS, GS, RVQ>::LB != 4;
+  const int64_t T1 = (a.n_groups + UMAX - 1) / UMAX;
+  const int w_rt = T1 <= 4 ? 4 : (T1 <= 8 ? 8 : (T1 <= 16 ? 16 : 0));
+  const bool rt2_shape = RT2_OK && a.M > 1 && w_rt > 0 && aligned(UMAX) &&
+                         ((g.tile_end[g.n - 1] + 1) / 2) * w_rt >= 2048;
+  // x staged in LDS when it fits, except for 4-bit codes at M >= 3 on the
+  // launches that read it from L2 faster (two row tiles per workgroup, or
+  // 8-wave straight-line): 14336 x 4096 at M = 8 21.9 -> 18.6 us, 4096 x 4096
+  // at M = 6 8.0 -> 7.0 us (2- and 8-bit layers, and 4-bit layers that would
+  // take the looping kernel, keep staging)
+  const bool xlds = xfit && !(RT2_OK && a.M > 2 && (rt2_shape || (sh.ok && sh.W == 8 && aligned(UMAX))));
+  const bool rt2 = rt2_shape && !xlds;
   // x through registers when xreg_chunks(w) chunks per thread hold it
   auto xreg = [&](int w) { return xlds && (int64_t)a.M * a.K / 8 <= (int64_t)xreg_chunks(w) * 64 * w; };
   // M = 1: x through per-wave LDS slots when a batch's (group, MFMA) pairs fit
@@ -1097,14 +1112,6 @@ inline int launch_decode(const DecodeGroup& g, hipStream_t st) {
   constexpr bool SLOT_OK = UMAX * ((BITS == 8 && CB8) ? GS / 16 : GS / 32) <= 16;
   const bool slot = SLOT_OK && a.M == 1;
   const bool one = (a.n_groups + UMAX - 1) / UMAX <= sh.W;  // one batch per wave
-  // x from global memory at M > 1 with at least half a resident round of
-  // waves: two row tiles per workgroup share each x fragment (4-bit codes),
-  // W the smallest of {4, 8, 16} that gives one batch per wave
-  constexpr bool RT2_OK = BITS == 4 && !RVQ && !CB8 && DecGeom<BITS, GS, RVQ>::LB != 4;
-  const int64_t T1 = (a.n_groups + UMAX - 1) / UMAX;
-  const int w_rt = T1 <= 4 ? 4 : (T1 <= 8 ? 8 : (T1 <= 16 ? 16 : 0));
-  const bool rt2 = RT2_OK && !xlds && a.M > 1 && w_rt > 0 && aligned(UMAX) &&
-                   ((g.tile_end[g.n - 1] + 1) / 2) * w_rt >= 2048;
 #define TS_DEC(XMV, DQV, ALV, WV, UV, LP) \
   return launch_decode_x<BITS, GS, BF16, CB8, RVQ, REP, XMV, DQV, ALV, WV, UV, (LP) ? 0 : 2>(g, st)
 #define TS_DEC1(XMV, DQV, ALV, WV, UV) \
