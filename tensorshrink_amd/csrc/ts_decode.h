@@ -51,6 +51,7 @@
 //   * LDS barriers wait for LDS traffic only (ts_lds_barrier), never for the
 //     weight loads in flight.
 #pragma once
+#include <utility>
 #include <algorithm>
 
 #include "ts_common.h"
@@ -88,8 +89,9 @@ struct DecodeArgs {
   int64_t n_tiles;
   int M;
   const float* cbsrc;        // codebook (read when cb_mode == CB_DEVICE)
-  int cb_mode;               // CB_UNIFORM, CB_INLINE (values in cbv) or CB_DEVICE
-  float cbv[16];             // the codebook with CB_INLINE
+  int cb_mode;               // CB_UNIFORM, CB_INLINE or CB_DEVICE
+  uint32_t cbq[16];          // CB_UNIFORM / CB_INLINE: entry j - cb0 in the activation type (bits in 0..15)
+  float cb0;                 // the centre subtracted from cbq (0 for uniform grids and RVQ stage 1)
   const uint16_t* bias_src;  // bias, or any valid array when there is none
   int64_t bias_mul;          // 1 with a bias, else 0
 };
@@ -121,6 +123,17 @@ enum { XM_GLOBAL = 0, XM_DMA = 1, XM_REG = 2, XM_SLOT = 3 };
 // 16-byte x chunks per thread with XM_REG: 4 with 8 or 16 waves (x up to
 // 32 / 64 KB: a 14336- / 28672-wide row at M = 1), else 2.
 constexpr int xreg_chunks(int w) { return w >= 8 ? 4 : 2; }
+
+// v_writelane_b32 of v[J] into lane J of q for every J (lane selects are
+// inline constants; the values come from SGPRs)
+template <int J>
+TS_DEV void ts_writelane(int& q, uint32_t v) {
+  asm("v_writelane_b32 %0, %1, %2" : "+v"(q) : "s"(v), "I"(J));
+}
+template <int... J>
+TS_DEV void ts_writelanes(int& q, const uint32_t* v, std::integer_sequence<int, J...>) {
+  (ts_writelane<J>(q, v[J]), ...);
+}
 
 template <bool BF16>
 TS_DEV uint32_t pack2(float lo, float hi) {
@@ -259,7 +272,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   TS_PG(packed); TS_PG(scale); TS_PG(gmin); TS_PG(dqsc); TS_PG(dqsm); TS_PG(dqgc); TS_PG(dqgm); TS_PG(x); TS_PG(y);
   TS_PG(slots); TS_PG(cbsrc); TS_PG(bias_src);
   TS_PS(pstride); TS_PS(dq_gs); TS_PS(dqm_bytes); TS_PS(ldx); TS_PS(ldy); TS_PS(N); TS_PS(cols); TS_PS(K); TS_PS(n_groups);
-  TS_PS(n_tiles); TS_PS(M); TS_PS(cb_mode); TS_PS(cap); TS_PS(bias_mul); TS_PS(y_dtype);
+  TS_PS(n_tiles); TS_PS(M); TS_PS(cb_mode); TS_PS(cap); TS_PS(bias_mul); TS_PS(y_dtype); TS_PS(cb0);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) TS_PS(cbq[j]);
   if constexpr (RVQ) { TS_PG(s2packed); TS_PS(s2stride); TS_PG(s2scale); TS_PG(s2gmin); }
 #undef TS_PG
 #undef TS_PS
@@ -717,6 +732,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
     }
   }
   constexpr int NCB = 1 << (RVQ ? 4 : BITS);
+  // Codebooks of at most 16 entries and uniform grids come as launch
+  // arguments (cbq), already centred and rounded to the activation type, so
+  // the 2- and 4-bit tables are built from them directly: lane j < 16 of qv
+  // holds entry j and each table word gathers its entries with ds_bpermute.
+  // No staging store, barrier or rounding sits before the weight stream. A
+  // device codebook (and the 8-bit table) is staged in cbs first.
+  const bool argcb = a.cb_mode != CB_DEVICE && !USE_T8;  // the same for the whole workgroup
   const int cbi = tid & 255;  // staged codebook slot (every writer of a slot writes the same value)
   // Codebook value of slot cbi. The device read is the only load behind a
   // (uniform) branch: on the other paths no load is issued there, and the
@@ -728,13 +750,11 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   // unconditional store (threads tid, tid + 256, ... write the same value to
   // slot tid % 256): a store under `tid < NCB` would let the compiler sink
   // the codebook load next to it and wait there for every load issued before.
-  if (a.cb_mode == CB_INLINE) {
-    float v = a.cbv[0];
-#pragma unroll
-    for (int j = 1; j < 16; ++j) v = cbi == j ? a.cbv[j] : v;
-    cbv = v;
-  }
   cbs[cbi] = cbv;
+  int qv = 0;
+  if (argcb) ts_writelanes(qv, a.cbq, std::make_integer_sequence<int, 16>{});
+  // entry j of the argument codebook (every lane of the wave active)
+  auto cq = [&](int j) { return (uint32_t)__builtin_amdgcn_ds_bpermute(j << 2, qv); };
   if constexpr (XM == XM_REG) {
     // unconditional stores (a thread past the end rewrites the last chunk
     // with the same bytes): a store under a predicate would let the compiler
@@ -771,17 +791,28 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       }
     }
   }
-  ts_lds_barrier();
+  // x staging (XM_REG, XM_DMA) and the staged codebook are read across waves
+  if (XM == XM_REG || XM == XM_DMA || !argcb) ts_lds_barrier();
   if constexpr (CENTER) {
-    if (a.cb_mode != CB_UNIFORM) c0 = 0.5f * (cbs[0] + cbs[NCB - 1]);
+    if (argcb) c0 = a.cb0;
+    else if (a.cb_mode != CB_UNIFORM) c0 = 0.5f * (cbs[0] + cbs[NCB - 1]);
   }
   // entry b's R copies are contiguous: 16-byte stores of four (u32 entries)
-  // or two (u64 entries) copies at a time
+  // or two (u64 entries) copies at a time. Every loop below runs whole waves
+  // (256 R entries, a multiple of 64 per step), as the gathers need.
   if constexpr (USE_T4 && !USE_T2 && R % 4 == 0) {
-    for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
-      const int b = e / R;
-      const uint32_t v = pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
-      *reinterpret_cast<ts_u32x4*>(t4 + e) = ts_u32x4{v, v, v, v};
+    if (argcb) {
+      for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
+        const int b = e / R;
+        const uint32_t v = cq(b & 15) | (cq(b >> 4) << 16);
+        *reinterpret_cast<ts_u32x4*>(t4 + e) = ts_u32x4{v, v, v, v};
+      }
+    } else {
+      for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
+        const int b = e / R;
+        const uint32_t v = pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
+        *reinterpret_cast<ts_u32x4*>(t4 + e) = ts_u32x4{v, v, v, v};
+      }
     }
   } else if constexpr (USE_T8 && R % 4 == 0) {
     for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
@@ -792,25 +823,38 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       *reinterpret_cast<ts_u32x4*>(t8 + e) = ts_u32x4{w, w, w, w};
     }
   } else if constexpr (USE_T2 && !USE_T4 && R % 2 == 0) {
-    for (int e = 2 * tid; e < 256 * R; e += 2 * NT) {
-      const int b = e / R;
-      float v[4];
-      for (int j = 0; j < 4; ++j) v[j] = cbs[(b >> (2 * j)) & 3] - c0;  // a 2-bit layer's codebook
-      const uint32_t lo = pack2<BF16>(v[0], v[1]), hi = pack2<BF16>(v[2], v[3]);
-      *reinterpret_cast<ts_u32x4*>(t2 + e) = ts_u32x4{lo, hi, lo, hi};
+    if (argcb) {
+      for (int e = 2 * tid; e < 256 * R; e += 2 * NT) {
+        const int b = e / R;
+        const uint32_t lo = cq(b & 3) | (cq((b >> 2) & 3) << 16), hi = cq((b >> 4) & 3) | (cq(b >> 6) << 16);
+        *reinterpret_cast<ts_u32x4*>(t2 + e) = ts_u32x4{lo, hi, lo, hi};
+      }
+    } else {
+      for (int e = 2 * tid; e < 256 * R; e += 2 * NT) {
+        const int b = e / R;
+        float v[4];
+        for (int j = 0; j < 4; ++j) v[j] = cbs[(b >> (2 * j)) & 3] - c0;  // a 2-bit layer's codebook
+        const uint32_t lo = pack2<BF16>(v[0], v[1]), hi = pack2<BF16>(v[2], v[3]);
+        *reinterpret_cast<ts_u32x4*>(t2 + e) = ts_u32x4{lo, hi, lo, hi};
+      }
     }
   } else
   for (int e = tid; e < 256 * R; e += NT) {
     const int b = e / R;
-    if constexpr (USE_T4) t4[e] = pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
+    if constexpr (USE_T4)
+      t4[e] = argcb ? cq(b & 15) | (cq(b >> 4) << 16) : pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
     if constexpr (USE_T2) {
       // RVQ stage 2 is always a uniform grid; a 2-bit layer uses its codebook.
-      float v[4];
-      for (int j = 0; j < 4; ++j) {
-        const int c = (b >> (2 * j)) & 3;
-        v[j] = RVQ ? (float)c : cbs[c] - c0;
+      if (!RVQ && argcb) {
+        t2[e] = make_uint2(cq(b & 3) | (cq((b >> 2) & 3) << 16), cq((b >> 4) & 3) | (cq(b >> 6) << 16));
+      } else {
+        float v[4];
+        for (int j = 0; j < 4; ++j) {
+          const int c = (b >> (2 * j)) & 3;
+          v[j] = RVQ ? (float)c : cbs[c] - c0;
+        }
+        t2[e] = make_uint2(pack2<BF16>(v[0], v[1]), pack2<BF16>(v[2], v[3]));
       }
-      t2[e] = make_uint2(pack2<BF16>(v[0], v[1]), pack2<BF16>(v[2], v[3]));
     }
     if constexpr (USE_T8) {
       const float v = cbs[b];

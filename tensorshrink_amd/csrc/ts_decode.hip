@@ -2,12 +2,30 @@
 // them to the per-bit-width dispatcher. The kernel itself is in ts_decode.h.
 #include "ts_decode.h"
 
+#include <cstring>
+
 namespace ts {
+
+// float -> bf16 / f16 bits, rounding to nearest even: the kernel's own
+// conversions (ts_f2bf, and the f16 cast), here on the host.
+static uint16_t host_f2bf(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+static uint16_t host_f2h(float f) {
+  const _Float16 h = (_Float16)f;
+  uint16_t u;
+  std::memcpy(&u, &h, 2);
+  return u;
+}
 
 // Kernel arguments of one layer; NOT_COVERED when it has outliers but
 // neither per-tile outlier slots nor the CSR row offsets.
-static int fill_args(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, void* y, int64_t ldy,
-                     int y_dtype, const uint16_t* bias, DecodeArgs& a, DecodeCsr& c) {
+static int fill_args(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
+                     int64_t ldy, int y_dtype, const uint16_t* bias, DecodeArgs& a, DecodeCsr& c) {
   a = DecodeArgs{};
   a.packed = L->packed;
   a.pstride = L->packed_stride;
@@ -40,8 +58,17 @@ static int fill_args(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t l
   a.cbsrc = L->codebook ? L->codebook : static_cast<const float*>(dummy);
   const int ncb = 1 << (L->bits == 6 ? 4 : L->bits);
   a.cb_mode = !L->codebook ? CB_UNIFORM : (L->codebook_host && ncb <= 16) ? CB_INLINE : CB_DEVICE;
-  if (a.cb_mode == CB_INLINE)
-    for (int j = 0; j < 16; ++j) a.cbv[j] = L->codebook_host[j < ncb ? j : 0];
+  if (a.cb_mode != CB_DEVICE) {
+    // The table entries, as the kernel uses them: centred on the middle of
+    // the codebook's range, cb0 = (cb[0] + cb[last]) / 2, for 2- and 4-bit
+    // codebooks (NF, Lloyd-Max; uniform grids and RVQ stage 1 keep cb0 = 0),
+    // then rounded to the activation type.
+    float v[16];
+    for (int j = 0; j < 16; ++j) v[j] = a.cb_mode == CB_INLINE ? L->codebook_host[j < ncb ? j : 0] : (float)j;
+    const bool centre = a.cb_mode == CB_INLINE && (L->bits == 4 || L->bits == 2);
+    a.cb0 = centre ? 0.5f * (v[0] + v[ncb - 1]) : 0.f;
+    for (int j = 0; j < 16; ++j) a.cbq[j] = x_dtype == TS_BF16 ? host_f2bf(v[j] - a.cb0) : host_f2h(v[j] - a.cb0);
+  }
   a.x = x;
   a.ldx = ldx;
   a.y = y;
@@ -80,7 +107,7 @@ static int dispatch(const ts_qlayer* L, DecodeGroup& g, bool bf16, hipStream_t s
 int decode_forward(const ts_qlayer* L, const uint16_t* x, int64_t M, int64_t ldx, int x_dtype, void* y,
                    int64_t ldy, int y_dtype, const uint16_t* bias, hipStream_t st) {
   DecodeGroup g{};
-  const int rc = fill_args(L, x, M, ldx, y, ldy, y_dtype, bias, g.a[0], g.csr[0]);
+  const int rc = fill_args(L, x, M, ldx, x_dtype, y, ldy, y_dtype, bias, g.a[0], g.csr[0]);
   if (rc != TS_OK) return rc;
   g.tile_end[0] = g.a[0].n_tiles;
   g.n = 1;
@@ -106,7 +133,7 @@ int decode_forward_group(const ts_qlayer* const* layers, int n, const uint16_t* 
   for (int l = 0; l < n; ++l) {
     if (!same_format(layers[0], layers[l])) return TS_NOT_COVERED;
     const int rc =
-        fill_args(layers[l], x, M, ldx, y[l], ldy[l], y_dtype, bias ? bias[l] : nullptr, g.a[l], g.csr[l]);
+        fill_args(layers[l], x, M, ldx, x_dtype, y[l], ldy[l], y_dtype, bias ? bias[l] : nullptr, g.a[l], g.csr[l]);
     if (rc != TS_OK) return rc;
     tiles += g.a[l].n_tiles;
     g.tile_end[l] = tiles;

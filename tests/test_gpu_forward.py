@@ -229,6 +229,35 @@ def test_cfg5_llama70b_layer_decode():
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fmt", ["nf4_dq", "lloyd2"])
+def test_decode_device_codebook_matches_launch_args(fmt, dtype):
+    """The kernel-level API passes the codebook as a device tensor, so the
+    decode kernel stages it and centres / rounds the table entries on the
+    GPU; QuantLinear passes a host copy, whose entries are centred and rounded
+    on the host and go in as launch arguments. Both must give the same tables:
+    identical outputs at decode sizes, for bf16 and f16 activations."""
+    ts = _ts()
+    opts = NF4 if fmt == "nf4_dq" else dict(bits=2, group_size=64, outlier_frac=0.001, companded=True)
+    ql = ts.QuantLinear(ts.quantize_tensor(recipes.student_t_weight(520, 1024, 31), **opts))
+    assert ql.codebook is not None
+    dq = bool(opts.get("double_quant"))
+    for M in (1, 5, 16):
+        x = recipes.activations(M, 1024, seed=M, dtype=dtype).cuda()
+        kw = dict(codebook=ql.codebook, outlier_row=ql.outlier_row, outlier_col=ql.outlier_col,
+                  outlier_delta=ql.outlier_delta, n_groups=ql.n_groups)
+        if dq:
+            kw.update(dq_scale_codes=ql.dq_scale_codes, dq_scale_meta=ql.dq_scale_meta,
+                      dq_gmin_codes=ql.dq_gmin_codes, dq_gmin_meta=ql.dq_gmin_meta, dq_group_size=ql.dq_group_size)
+        y_dev = ts.fused_quantized_linear(x, ql.packed, None if dq else ql.scale, None if dq else ql.gmin, None,
+                                          opts["bits"], opts["group_size"], ql.cols, ql.out_features, dtype, **kw)
+        y_arg = ql(x)
+        torch.cuda.synchronize()
+        say("device codebook", fmt, dtype, M)
+        assert y_dev is not None and y_dev.dtype == dtype
+        assert torch.equal(y_dev, y_arg), (fmt, dtype, M)
+
+
 def test_kernel_api_functions():
     ts = _ts()
     spec, res, d, w = load_case("u4_dq_g128_bias")
