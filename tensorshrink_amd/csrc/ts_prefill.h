@@ -295,7 +295,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
   // Per-group scale and offset of a stage (float32; modules.py:573-579 for
   // the double-quant codes: code * meta_scale + meta_min).
   struct Scales {
-    float s[NGT], g[NGT], s2[NGT], g2[NGT];
+    float s[NGT], g[NGT], s2[NGT], gg[NGT];  // gg: g + stage-2 gmin (RVQ)
   };
   auto scales = [&](const Stage& S, Scales& Q) {
 #pragma unroll
@@ -309,7 +309,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
       }
       if constexpr (RVQ) {
         Q.s2[t] = ts_h2f((uint16_t)(S.s2[t] & 0xffffu));
-        Q.g2[t] = ts_h2f((uint16_t)(S.s2[t] >> 16));
+        Q.gg[t] = Q.g[t] + ts_h2f((uint16_t)(S.s2[t] >> 16));
       }
     }
   };
@@ -382,12 +382,23 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_kernel(const PrefillArgs a
         for (int e = 0; e < 8; ++e) cv[e] = (float)((S.w[c8 >> 1] >> (16 * (c8 & 1) + 2 * e)) & 3u);
       }
       float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(cv[e], sc, gm);
       if constexpr (RVQ) {
+        // both stages in one affine per element, c1 s + (c2 s2 + (g + g2)):
+        // byte 0 of q[k] holds stage-2 code k and byte 1 code k + 4, so each
+        // conversion is a byte-select one (v_cvt_f32_ubyteN)
         const uint32_t d2 = S.w2[c8 >> 1] >> (16 * (c8 & 1));
+        uint32_t q[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] += __builtin_fmaf((float)((d2 >> (2 * e)) & 3u), Q.s2[t], Q.g2[t]);
+        for (int k = 0; k < 4; ++k) q[k] = (d2 >> (2 * k)) & 0x0303u;
+        asm volatile("" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float c2 = (float)((q[e & 3] >> (8 * (e >> 2))) & 0xffu);
+          v[e] = __builtin_fmaf(cv[e], sc, __builtin_fmaf(c2, Q.s2[t], Q.gg[t]));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(cv[e], sc, gm);
       }
       ts_u32x4 pk;
       pk.x = to_pair<BF16>(v[0], v[1]);
