@@ -358,6 +358,26 @@ def load_traffic(units):
         return None
 
 
+def decode_counter_launches(n=50):
+    """Eager M = 1 forwards for SQ-counter runs (no graphs, no timing): the
+    config-2 layer (2-bit Lloyd-Max, group 64), a 4096 x 4096 and a 14336 x
+    4096 NF4 + double-quant layer, n launches each."""
+    import recipes
+    import tensorshrink_amd as ts
+    nf4 = dict(bits=4, group_size=128, outlier_frac=0.001, double_quant=True, nf_quant=True)
+    lm2 = dict(bits=2, group_size=64, outlier_frac=0.001, companded=True)
+    for name, fmt, rows, cols in (("cfg2", lm2, 11008, 4096), ("nf4_4096", nf4, 4096, 4096),
+                                  ("nf4_14336", nf4, 14336, 4096)):
+        torch.manual_seed(1)
+        ql = ts.QuantLinear(ts.quantize_tensor(recipes.gaussian_weight(rows, cols, 3), **fmt))
+        x = recipes.activations(1, cols, seed=1).cuda()
+        for _ in range(n):
+            ql(x)
+        torch.cuda.synchronize()
+        log(f"decode counters: {name} x {n}")
+        del ql
+
+
 def copy_calibration():
     """A plain device copy of known size, for scaling FETCH_SIZE/WRITE_SIZE."""
     n = 512 * 1024 * 1024
@@ -623,6 +643,8 @@ def main():
     ap.add_argument("--quantize-reps", type=int, default=3)
     ap.add_argument("--copy-calib", action="store_true", help="only run the plain-copy PMC calibration")
     ap.add_argument("--prefill-only", action="store_true", help="only the prefill lines (for counter runs)")
+    ap.add_argument("--decode-counters", action="store_true",
+                    help="only eager M=1 decode launches of three layers (for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build targets a single MI355X and has no multi-GPU path "
@@ -632,6 +654,9 @@ def main():
     torch.cuda.set_device(0)
     if args.copy_calib:
         copy_calibration()
+        return
+    if args.decode_counters:
+        decode_counter_launches()
         return
     if args.prefill_only:
         pre = bench_prefill(args)
