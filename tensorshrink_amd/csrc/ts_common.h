@@ -134,11 +134,18 @@ __host__ __device__ inline int64_t ts_cdiv(int64_t a, int64_t b) { return (a + b
 
 // Raises a kernel's dynamic LDS limit once per device, thread safe: each
 // caller owns a flags/ok pair of 64 entries (one per device ordinal).
-inline bool ts_set_smem_once(const void* kern, size_t smem, std::once_flag* flags, bool* ok) {
+// lds_at_zero: the kernel addresses its dynamic LDS from offset 0, so it
+// must have no static LDS (checked once, like the attribute).
+inline bool ts_set_smem_once(const void* kern, size_t smem, std::once_flag* flags, bool* ok,
+                             bool lds_at_zero = false) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
   std::call_once(flags[dev], [&] {
     ok[dev] = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) == hipSuccess;
+    if (ok[dev] && lds_at_zero) {
+      hipFuncAttributes fa{};
+      ok[dev] = hipFuncGetAttributes(&fa, kern) == hipSuccess && fa.sharedSizeBytes == 0;
+    }
   });
   return ok[dev];
 }

@@ -249,6 +249,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   constexpr bool TQ = LB == 4 && !RVQ && U % 4 == 0;            // quarter-transposed code loads
   constexpr int CPM = (BITS == 8 && CB8) ? 4 : 8;              // codes per lane per MFMA
   constexpr bool USE_T4 = (BITS == 4);
+  // 16-wave launches at M = 1 (one workgroup per CU, LDS to spare): entry b's
+  // copies sit in a 256-byte row of the table, so a lookup's byte address,
+  // (b << 8) | 4 rsl, is one v_perm_b32 of the code dword instead of a
+  // byte extract and an add
+  constexpr bool T4W = USE_T4 && !RVQ && XM == XM_SLOT && W == 16;
+  constexpr int T4S = T4W ? 64 : R;  // table words between entries
+  static_assert(!T4W || R <= 64, "4 rsl fits the address's low byte");
   constexpr bool USE_T2 = (BITS == 2) || RVQ;
   constexpr bool USE_T8 = (BITS == 8) && CB8;
   constexpr int NW8 = (U + 3) / 4;   // words holding U bytes
@@ -285,13 +292,14 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   const int n = lane & 15;
   const int q = lane >> 4;
   const int rsl = lane & (R - 1);
+  const uint32_t rsl4 = 4u * (uint32_t)rsl;
 
   // ---- LDS carve-up ------------------------------------------------------
   unsigned char* sp = smem;
   uint32_t* t4 = nullptr;
   uint2* t2 = nullptr;
   uint32_t* t8 = nullptr;
-  if constexpr (USE_T4) { t4 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
+  if constexpr (USE_T4) { t4 = reinterpret_cast<uint32_t*>(sp); sp += 256 * T4S * 4; }
   if constexpr (USE_T2) { t2 = reinterpret_cast<uint2*>(sp); sp += 256 * R * 8; }
   if constexpr (USE_T8) { t8 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
   float* red = reinterpret_cast<float*>(sp);       // [MB][RT][W][64][4]
@@ -550,7 +558,16 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
           xa[j] = ts_u32x4{__builtin_amdgcn_perm(v.x, v.x, 0x05040100u), __builtin_amdgcn_perm(v.x, v.x, 0x07060302u),
                            __builtin_amdgcn_perm(v.y, v.y, 0x05040100u), __builtin_amdgcn_perm(v.y, v.y, 0x07060302u)};
         }
-        if constexpr (BITS == 4) {
+        if constexpr (T4W) {
+          // byte t of code dword j to address byte 1, 4 rsl to byte 0: the
+          // LDS byte address itself (the table is at offset 0 of the
+          // workgroup's LDS, which the launch checks: no static LDS)
+          using lds_u32 = const __attribute__((address_space(3))) uint32_t;
+          auto lk = [&](uint32_t sel) {
+            return *reinterpret_cast<lds_u32*>((uintptr_t)__builtin_amdgcn_perm(wd[j], rsl4, sel));
+          };
+          bv[j] = ts_u32x4{lk(0x0c0c0400u), lk(0x0c0c0500u), lk(0x0c0c0600u), lk(0x0c0c0700u)};
+        } else if constexpr (BITS == 4) {
           const int b0 = 4 * j;
           bv[j] = ts_u32x4{t4[byte_of(wd, b0 + 0) * R + rsl], t4[byte_of(wd, b0 + 1) * R + rsl],
                            t4[byte_of(wd, b0 + 2) * R + rsl], t4[byte_of(wd, b0 + 3) * R + rsl]};
@@ -805,13 +822,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
       for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
         const int b = e / R;
         const uint32_t v = cq(b & 15) | (cq(b >> 4) << 16);
-        *reinterpret_cast<ts_u32x4*>(t4 + e) = ts_u32x4{v, v, v, v};
+        *reinterpret_cast<ts_u32x4*>(t4 + b * T4S + (e - b * R)) = ts_u32x4{v, v, v, v};
       }
     } else {
       for (int e = 4 * tid; e < 256 * R; e += 4 * NT) {
         const int b = e / R;
         const uint32_t v = pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
-        *reinterpret_cast<ts_u32x4*>(t4 + e) = ts_u32x4{v, v, v, v};
+        *reinterpret_cast<ts_u32x4*>(t4 + b * T4S + (e - b * R)) = ts_u32x4{v, v, v, v};
       }
     }
   } else if constexpr (USE_T8 && R % 4 == 0) {
@@ -842,7 +859,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   for (int e = tid; e < 256 * R; e += NT) {
     const int b = e / R;
     if constexpr (USE_T4)
-      t4[e] = argcb ? cq(b & 15) | (cq(b >> 4) << 16) : pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
+      t4[b * T4S + (e - b * R)] =
+          argcb ? cq(b & 15) | (cq(b >> 4) << 16) : pack2<BF16>(cbs[b & 15] - c0, cbs[b >> 4] - c0);
     if constexpr (USE_T2) {
       // RVQ stage 2 is always a uniform grid; a 2-bit layer uses its codebook.
       if (!RVQ && argcb) {
@@ -1047,8 +1065,9 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
 template <int BITS, bool CB8, bool RVQ, int REP, int XM, int W, int RT, int MB = 1>
 inline size_t decode_smem(int M, int64_t K, bool xlds) {
   constexpr int R = dec_rep_x(REP, W, XM);
+  constexpr bool T4W = BITS == 4 && !RVQ && XM == XM_SLOT && W == 16;  // the kernel's wide table rows
   size_t s = 0;
-  if (BITS == 4) s += 256 * R * 4;
+  if (BITS == 4) s += 256 * (T4W ? 64 : R) * 4;
   if (BITS == 2 || RVQ) s += 256 * R * 8;
   if (BITS == 8 && CB8) s += 256 * R * 4;
   s += (size_t)MB * RT * W * 64 * 16;
@@ -1075,7 +1094,8 @@ inline int launch_decode_x(const DecodeGroup& g_in, hipStream_t st) {
   auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB, RT, MB>;
   static std::once_flag flags[64];
   static bool ok[64];
-  if (!ts_set_smem_once(reinterpret_cast<const void*>(kern), 160 * 1024, flags, ok)) return TS_HIP_ERROR;
+  constexpr bool T4W = BITS == 4 && !RVQ && XM == XM_SLOT && W == 16;  // table addressed from LDS offset 0
+  if (!ts_set_smem_once(reinterpret_cast<const void*>(kern), 160 * 1024, flags, ok, T4W)) return TS_HIP_ERROR;
   // one workgroup per 16-row tile; tiles beyond the resident capacity are
   // scheduled by the hardware as workgroups retire
   hipLaunchKernelGGL(kern, dim3((unsigned)g.tile_end[g.n - 1]), dim3(64 * W), smem, st, g);
