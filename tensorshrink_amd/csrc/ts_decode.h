@@ -197,6 +197,9 @@ TS_DEV uint32_t half_of(const uint32_t* d, int i) { return (d[i >> 1] >> (16 * (
 constexpr int dec_rep(int rep, int w) { return rep >= 32 ? (w >= 16 ? 32 : (w >= 8 ? 16 : 4)) : rep; }
 // With x in per-wave slots (XM_SLOT) the LDS holds the tables and 1 KB per wave: four 4-wave
 // workgroups per CU fit 16 copies each.
+// M = 1 launches of 8 or 16 waves (one or two workgroups per CU) lay the
+// 4-bit code table out in 256-byte rows (see the kernel)
+constexpr bool dec_t4w(int bits, bool rvq, int xm, int w) { return bits == 4 && !rvq && xm == 3 && w >= 8; }
 constexpr int dec_rep_x(int rep, int w, int xm) { return (xm == 3 && rep >= 32 && w == 4) ? 16 : dec_rep(rep, w); }
 
 template <int BITS, int GS, bool RVQ>
@@ -249,11 +252,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   constexpr bool TQ = LB == 4 && !RVQ && U % 4 == 0;            // quarter-transposed code loads
   constexpr int CPM = (BITS == 8 && CB8) ? 4 : 8;              // codes per lane per MFMA
   constexpr bool USE_T4 = (BITS == 4);
-  // 16-wave launches at M = 1 (one workgroup per CU, LDS to spare): entry b's
-  // copies sit in a 256-byte row of the table, so a lookup's byte address,
-  // (b << 8) | 4 rsl, is one v_perm_b32 of the code dword instead of a
-  // byte extract and an add
-  constexpr bool T4W = USE_T4 && !RVQ && XM == XM_SLOT && W == 16;
+  // 8- and 16-wave launches at M = 1 (one or two workgroups per CU): entry
+  // b's copies sit in a 256-byte row of the table, so a lookup's byte
+  // address, (b << 8) | 4 rsl, is one v_perm_b32 of the code dword instead
+  // of a byte extract and an add. The staged codebook then shares the
+  // partials buffer (read before the table barrier, which every partial is
+  // written after), so that two 8-wave workgroups fit a CU.
+  constexpr bool T4W = dec_t4w(BITS, RVQ, XM, W);
   constexpr int T4S = T4W ? 64 : R;  // table words between entries
   static_assert(!T4W || R <= 64, "4 rsl fits the address's low byte");
   constexpr bool USE_T2 = (BITS == 2) || RVQ;
@@ -304,8 +309,8 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
   if constexpr (USE_T8) { t8 = reinterpret_cast<uint32_t*>(sp); sp += 256 * R * 4; }
   float* red = reinterpret_cast<float*>(sp);       // [MB][RT][W][64][4]
   sp += MB * RT * W * 64 * 4 * 4;
-  float* cbs = reinterpret_cast<float*>(sp);       // [256] staged codebook
-  sp += 256 * 4;
+  float* cbs = T4W ? red : reinterpret_cast<float*>(sp);  // [256] staged codebook
+  if constexpr (!T4W) sp += 256 * 4;
   // XM_SLOT: each wave's x slot (64 lanes x 16 bytes)
   uint16_t* xw = reinterpret_cast<uint16_t*>(sp) + wave * 512;
   if constexpr (XM == XM_SLOT) sp += W * 1024;
@@ -1065,13 +1070,13 @@ __global__ __launch_bounds__(64 * W, 4) void decode_kernel(const DecodeGroup g) 
 template <int BITS, bool CB8, bool RVQ, int REP, int XM, int W, int RT, int MB = 1>
 inline size_t decode_smem(int M, int64_t K, bool xlds) {
   constexpr int R = dec_rep_x(REP, W, XM);
-  constexpr bool T4W = BITS == 4 && !RVQ && XM == XM_SLOT && W == 16;  // the kernel's wide table rows
+  constexpr bool T4W = dec_t4w(BITS, RVQ, XM, W);  // the kernel's wide table rows
   size_t s = 0;
   if (BITS == 4) s += 256 * (T4W ? 64 : R) * 4;
   if (BITS == 2 || RVQ) s += 256 * R * 8;
   if (BITS == 8 && CB8) s += 256 * R * 4;
   s += (size_t)MB * RT * W * 64 * 16;
-  s += 256 * 4;
+  if (!T4W) s += 256 * 4;  // staged codebook (inside the partials with T4W)
   if (XM == XM_SLOT) s += (size_t)W * 1024;
   if (xlds) s += ((size_t)M * K * 2 + 1023) / 1024 * 1024;  // whole 1 KB chunks
   return s;
@@ -1094,7 +1099,7 @@ inline int launch_decode_x(const DecodeGroup& g_in, hipStream_t st) {
   auto kern = decode_kernel<BITS, GS, BF16, CB8, RVQ, REP, XM, DQ, AL, W, U, NB, RT, MB>;
   static std::once_flag flags[64];
   static bool ok[64];
-  constexpr bool T4W = BITS == 4 && !RVQ && XM == XM_SLOT && W == 16;  // table addressed from LDS offset 0
+  constexpr bool T4W = dec_t4w(BITS, RVQ, XM, W);  // table addressed from LDS offset 0
   if (!ts_set_smem_once(reinterpret_cast<const void*>(kern), 160 * 1024, flags, ok, T4W)) return TS_HIP_ERROR;
   // one workgroup per 16-row tile; tiles beyond the resident capacity are
   // scheduled by the hardware as workgroups retire
