@@ -229,21 +229,27 @@ def test_cfg5_llama70b_layer_decode():
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("shape", [(520, 1024), (4096, 4096), (1024, 8192)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("fmt", ["nf4_dq", "lloyd2"])
-def test_decode_device_codebook_matches_launch_args(fmt, dtype):
+def test_decode_device_codebook_matches_launch_args(fmt, dtype, shape):
     """The kernel-level API passes the codebook as a device tensor, so the
     decode kernel stages it and centres / rounds the table entries on the
     GPU; QuantLinear passes a host copy, whose entries are centred and rounded
     on the host and go in as launch arguments. Both must give the same tables:
-    identical outputs at decode sizes, for bf16 and f16 activations."""
+    identical outputs at decode sizes, for bf16 and f16 activations. At M = 1
+    the 4-bit layers take 4-wave workgroups (520 x 1024, packed table),
+    8-wave ones (4096 x 4096) and 16-wave ones (1024 x 8192); the last two
+    use 256-byte table rows and stage the device codebook in the partials
+    buffer."""
     ts = _ts()
+    rows, cols = shape
     opts = NF4 if fmt == "nf4_dq" else dict(bits=2, group_size=64, outlier_frac=0.001, companded=True)
-    ql = ts.QuantLinear(ts.quantize_tensor(recipes.student_t_weight(520, 1024, 31), **opts))
+    ql = ts.QuantLinear(ts.quantize_tensor(recipes.student_t_weight(rows, cols, 31), **opts))
     assert ql.codebook is not None
     dq = bool(opts.get("double_quant"))
     for M in (1, 5, 16):
-        x = recipes.activations(M, 1024, seed=M, dtype=dtype).cuda()
+        x = recipes.activations(M, cols, seed=M, dtype=dtype).cuda()
         kw = dict(codebook=ql.codebook, outlier_row=ql.outlier_row, outlier_col=ql.outlier_col,
                   outlier_delta=ql.outlier_delta, n_groups=ql.n_groups)
         if dq:
@@ -253,9 +259,9 @@ def test_decode_device_codebook_matches_launch_args(fmt, dtype):
                                           opts["bits"], opts["group_size"], ql.cols, ql.out_features, dtype, **kw)
         y_arg = ql(x)
         torch.cuda.synchronize()
-        say("device codebook", fmt, dtype, M)
+        say("device codebook", fmt, dtype, shape, M)
         assert y_dev is not None and y_dev.dtype == dtype
-        assert torch.equal(y_dev, y_arg), (fmt, dtype, M)
+        assert torch.equal(y_dev, y_arg), (fmt, dtype, shape, M)
 
 
 def test_kernel_api_functions():
